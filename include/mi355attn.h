@@ -1,0 +1,116 @@
+/*
+ * mi355attn.h — C-ABI of libmi355attn.so, the gfx950 (MI355X) attention-block hot path.
+ *
+ * The reference implements this path as Python/PyTorch ops plus Triton kernels; its only native
+ * binding is the inline CUDA extension `nq_launch(int cfg, Tensor X, W, Bias, LnW, LnB, Out,
+ * int64 tokens, int64 D)` launched on the current stream
+ * (Project/kernels/k024_cuda_tuned.py:201-245). Every entry point below replaces one stage of
+ * `BaselineSelfAttention.forward` (torch_transformer_benchmark.py:85-122) or of its optimised
+ * restatements, and is cited at its declaration.
+ *
+ * Conventions (all entry points):
+ *   - plain device pointers, element strides and sizes; no framework types;
+ *   - `stream` is a hipStream_t passed as void* (NULL = the legacy default stream); kernels are
+ *     enqueued asynchronously, nothing is allocated, nothing synchronises the host, so a caller
+ *     may capture the calls in a hipGraph;
+ *   - return 0 on success, a negative MI355_E* code on an argument error (nothing launched),
+ *     or a positive hipError_t from the launch.
+ */
+#ifndef MI355ATTN_H
+#define MI355ATTN_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* element types */
+#define MI355_F32 0
+#define MI355_F16 1
+#define MI355_BF16 2
+
+/* argument-error status codes (negative) */
+#define MI355_OK 0
+#define MI355_E_NULL_POINTER (-1)   /* a required pointer is NULL */
+#define MI355_E_BAD_SIZE (-2)       /* a size is negative or exceeds the supported range */
+#define MI355_E_BAD_DTYPE (-3)      /* dtype code not supported by this entry point */
+#define MI355_E_ALIGNMENT (-4)      /* pointer or leading dimension violates 16-byte vector access */
+#define MI355_E_HEAD_DIM (-5)       /* head_dim not in the supported set {64, 128} */
+#define MI355_E_UNSUPPORTED (-6)    /* argument combination not supported */
+
+/* Library version, e.g. 100 for 0.1.0. */
+int mi355_version(void);
+
+/* Static description of a status code (never NULL). */
+const char* mi355_status_string(int status);
+
+/*
+ * Dense projection  C[M,N] = A[M,K] · W[N,K]^T + bias[N]   (nn.Linear semantics).
+ * Replaces q_proj/k_proj/v_proj/out_proj (torch_transformer_benchmark.py:93-95, :118) and the
+ * packed-QKV F.linear of the optimised route (Project/submission/dispatcher_region.py:789-792,
+ * :1025, :1085). A and W share in_dtype (F32, F16, BF16); C has out_dtype (F16 or BF16 for
+ * 16-bit inputs, which may differ from in_dtype; F32 for F32 inputs). bias is fp32 or NULL.
+ * Accumulation and the bias add are fp32; C is rounded once (round-to-nearest-even).
+ * Rows m with row_valid[m] == 0 are written as exact zeros (the output-row mask of
+ * torch_transformer_benchmark.py:120-121); row_valid may be NULL (all rows valid).
+ * Requirements: K % (16 / sizeof(elem)) == 0, lda/ldw multiples of that, 16-byte aligned A, W.
+ */
+int mi355_gemm_bias(int in_dtype, int out_dtype, const void* A, int64_t lda, const void* W,
+                    int64_t ldw, const float* bias, void* C, int64_t ldc, int64_t M, int64_t N,
+                    int64_t K, const uint8_t* row_valid, void* stream);
+
+/*
+ * Streamed scaled-dot-product attention forward with online softmax; never forms S_q x S_k.
+ * Replaces scores/causal mask/key mask/softmax/P·V/head merge of BaselineSelfAttention.forward
+ * (torch_transformer_benchmark.py:97-117), the Triton kernels `_sub_attn_fwd` and
+ * `_sub_attn_heads` (Project/submission/dispatcher_region.py:217-291, :418-556) and the streamed
+ * oracle `streamed_attention` (Project/tools/shape14_eval.py:201-236).
+ *
+ * Q, K, V, O are 4-D [B, S, H, head_dim] views given by element strides (batch, seq, head);
+ * the head_dim stride must be 1. The packed [B, S, 3*d] QKV output of mi355_gemm_bias is read
+ * in place with seq stride 3*d. O is written in the caller's layout ([B, S, H, hd] makes the
+ * head merge free). Scores use `scale` (head_dim^-0.5 in the reference); softmax is fp32;
+ * probabilities are rounded to the input dtype before P·V (torch_transformer_benchmark.py:111).
+ * causal != 0 masks key j > query i (triu(diagonal=1), :99-103).
+ * key_valid (nullable) is a [B, S_k] byte mask with batch stride key_valid_sb; keys with 0 are
+ * excluded (:105-108). A query row whose keys are all excluded produces NaN, as softmax over an
+ * all -inf row does in the reference.
+ * Supported: dtype F32, F16, BF16 with head_dim 64 or 128.
+ */
+int mi355_attn_fwd(int dtype, const void* Q, const void* K, const void* V, void* O, int64_t B,
+                   int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim,
+                   const int64_t* q_strides, const int64_t* k_strides, const int64_t* v_strides,
+                   const int64_t* o_strides, float scale, int causal, const uint8_t* key_valid,
+                   int64_t key_valid_sb, void* stream);
+
+/*
+ * Per-row symmetric int8 quantisation of X[M,K] (row stride ldx) into Xq[M,K] (contiguous) and
+ * scale[M] (fp32). mode 0 = activation recipe `_quant_rows`
+ * (Project/kernels/k008_int8_gemm.py:148-151): s = max(amax, 1e-6) / 127.
+ * mode 1 = weight recipe `_int8_pack` (k008_int8_gemm.py:154-158): s = max(amax / 127, 1e-8).
+ * Both then store q = round_half_even(x / s) with IEEE fp32 division; X dtype is F32/F16/BF16
+ * (converted exactly to fp32 first). K % (16 / sizeof(elem)) == 0 and ldx likewise.
+ */
+int mi355_quant_rows_i8(int in_dtype, const void* X, int64_t ldx, int8_t* Xq, float* scale,
+                        int64_t M, int64_t K, int mode, void* stream);
+
+/*
+ * W8A8 projection: acc[M,N] = A_i8[M,K] · W_i8[N,K]^T in exact int32, then
+ * C = out_dtype( fp32(acc) * (s_a[m] * s_w[n]) + bias[n] ) with separately rounded fp32
+ * multiply/multiply/add, matching `_int8_linear` (Project/kernels/k008_int8_gemm.py:181-185;
+ * torch._int_mm + dequant). W is stored [N, K] (K contiguous) — the transpose of the
+ * reference's `[K, N]` cache (k008_int8_gemm.py:158) — so both MFMA operands are K-major.
+ * out_dtype is F32, F16 or BF16; bias (fp32) may be NULL; C may be NULL when acc_out is given.
+ * acc_out (nullable, [M,N] int32, row stride N) receives the raw accumulators before
+ * dequantisation. row_valid as for mi355_gemm_bias. K % 16 == 0, A and W contiguous rows.
+ */
+int mi355_gemm_i8(const int8_t* A, const int8_t* W, const float* s_a, const float* s_w,
+                  const float* bias, int out_dtype, void* C, int64_t ldc, int32_t* acc_out,
+                  int64_t M, int64_t N, int64_t K, const uint8_t* row_valid, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355ATTN_H */

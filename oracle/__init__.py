@@ -1,0 +1,26 @@
+"""CPU oracle for the attention-block hot path — TEST INFRASTRUCTURE ONLY.
+
+Only ``tests/``, ``__graft_entry__.smoke()`` and the ``cpu_baseline`` leg of ``bench.py`` may
+import this package, and only as the checker (or the timed CPU baseline). The product path
+(``tiktok_techjam_2026_track3_amd``) never imports it and has no CPU fallback.
+
+Contents (each function cites the reference file:line it restates):
+  attention.py  dense fp32 torch-CPU restatement of ``BaselineSelfAttention.forward`` and an
+                fp64 numpy brute force used to pin it;
+  streamed.py   chunk-wise online-softmax restatement of ``streamed_attention``;
+  int8.py       numpy restatement of the W8A8 recipe (``_quant_rows``, ``_int8_pack``,
+                ``_int8_linear``) with exact integer GEMM;
+  predicate.py  the elementwise ``abs <= atol OR abs <= rtol*|ref|`` comparator;
+  model.py      module-level restatement of the benchmark's transformer classes, used as the
+                ``otb`` argument of the plugin contract in tests.
+
+How each function is pinned (the reference ships no golden vectors for this path):
+  attention.self_attention     fp64 brute force (per-row loops) + closed-form special cases
+  attention.attention_core     same, plus softmax shift/permutation invariances
+  streamed.*                   equals the dense restatement (fp32 reassociation only)
+  int8.quant_rows / pack       hand-computed cases: zero row, row max -> +-127, .5 ties to even
+  int8.int8_gemm               brute-force int64 loops on small shapes
+  int8.int8_linear             hand-computed dequantisation on a 1x1x1 case
+  predicate.compare_outputs    hand-built cases for each clause (atol, rtol, NaN, inf)
+All pins live in tests/test_oracle.py.
+"""

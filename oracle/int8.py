@@ -1,0 +1,104 @@
+"""numpy restatement of the W8A8 int8 projection recipe — test infrastructure only.
+
+Restates Project/kernels/k008_int8_gemm.py:
+  ``_quant_rows``  (:148-151)  per-row activation scale  s = clamp(amax, 1e-6) / 127,
+                               q = round_half_even(t / s) -> int8;
+  ``_int8_pack``   (:154-158)  per-output-channel weight scale s = clamp(amax / 127, 1e-8);
+                               the reference stores W_i8 transposed [K, N]; this restatement
+                               returns [N, K] (the library's operand layout) — the integer
+                               values are identical;
+  ``_int8_linear`` (:181-185)  acc = A_i8 @ W_i8^T (torch._int_mm, exact int32),
+                               y = fp32(acc) * (s_a * s_w) + b in fp32, each op rounded.
+All arithmetic is float32 (IEEE, no fused multiply-add) exactly as torch performs it, so the
+library's outputs are compared bit for bit.
+
+``int8_gemm`` computes the integer product through float64 BLAS, which is exact because every
+partial sum is an integer of magnitude <= K * 128 * 128 < 2**53.
+"""
+from __future__ import annotations
+
+import numpy as np
+
+F32 = np.float32
+
+
+def quant_rows(t: np.ndarray):
+    """Activation recipe: returns (int8 [N, K], fp32 scale [N])."""
+    t = np.asarray(t, dtype=F32)
+    amax = np.abs(t).max(axis=-1)
+    s = (np.maximum(amax, F32(1e-6)) / F32(127.0)).astype(F32)
+    q = np.rint(t / s[:, None]).astype(np.int8)
+    return q, s
+
+
+def quant_weight(w: np.ndarray):
+    """Weight recipe: returns (int8 [N, K], fp32 scale [N])."""
+    w = np.asarray(w, dtype=F32)
+    s = np.maximum(np.abs(w).max(axis=1) / F32(127.0), F32(1e-8)).astype(F32)
+    q = np.rint(w / s[:, None]).astype(np.int8)
+    return q, s
+
+
+def int8_gemm(a_i8: np.ndarray, w_i8: np.ndarray) -> np.ndarray:
+    """Exact int32 accumulators of a_i8 [M, K] @ w_i8 [N, K]^T."""
+    a = np.asarray(a_i8)
+    w = np.asarray(w_i8)
+    K = a.shape[1]
+    if K * 128 * 128 >= 2 ** 53:
+        raise ValueError("K too large for exact float64 accumulation")
+    acc = a.astype(np.float64) @ w.astype(np.float64).T
+    return acc.astype(np.int64).astype(np.int32)
+
+
+def dequant(acc: np.ndarray, s_a: np.ndarray, s_w: np.ndarray, bias=None) -> np.ndarray:
+    """y = fp32(acc) * (s_a * s_w) + b, each operation rounded to fp32."""
+    y = np.asarray(acc).astype(F32)
+    sc = (np.asarray(s_a, F32)[:, None] * np.asarray(s_w, F32)[None, :]).astype(F32)
+    y = (y * sc).astype(F32)
+    if bias is not None:
+        y = (y + np.asarray(bias, F32)[None, :]).astype(F32)
+    return y
+
+
+def int8_linear(h: np.ndarray, w_i8: np.ndarray, s_w: np.ndarray, bias=None):
+    """h [N, K] fp32 -> (y fp32 [N, out], acc int32) via per-token quantisation."""
+    a8, s_a = quant_rows(h)
+    acc = int8_gemm(a8, w_i8)
+    return dequant(acc, s_a, s_w, bias), acc
+
+
+def pack_block(params):
+    """Quantised weights of one block: packed QKV [3d, d] and out-proj [d, d] (k008:161-178)."""
+    import torch  # local: keep the numpy recipe importable without torch
+    w_qkv = torch.cat([params[f"{n}.weight"].float() for n in ("q_proj", "k_proj", "v_proj")]).numpy()
+    b_qkv = torch.cat([params[f"{n}.bias"].float() for n in ("q_proj", "k_proj", "v_proj")]).numpy()
+    wq, sq = quant_weight(w_qkv)
+    wo, so = quant_weight(params["out_proj.weight"].float().numpy())
+    return {"qkv_w": wq, "qkv_s": sq, "qkv_b": b_qkv.astype(F32),
+            "out_w": wo, "out_s": so, "out_b": params["out_proj.bias"].float().numpy().astype(F32)}
+
+
+def int8_self_attention(x, params, num_heads: int, causal: bool = False, rows=None):
+    """The attention half of ``block_forward`` (k008_int8_gemm.py:189-223) on CPU.
+
+    x [B, S, d] (fp16 values) -> quantised QKV projection -> fp16 qkv (:197) -> fp32-math
+    attention -> context rounded to fp16 (the fp16 attention output, :207) -> quantised out
+    projection (:221). Returns a dict with the fp16 qkv, the fp16 context and the fp32 output;
+    ``rows`` optionally restricts the context/output to a subset of flattened token rows.
+    """
+    import torch
+    from .attention import attention_core
+
+    pk = pack_block(params)
+    B, S, d = x.shape
+    hd = d // num_heads
+    h = x.float().reshape(B * S, d).numpy()
+    qkv32, _ = int8_linear(h, pk["qkv_w"], pk["qkv_s"], pk["qkv_b"])
+    qkv16 = torch.from_numpy(qkv32.astype(np.float16))
+    q5 = qkv16.float().view(B, S, 3, num_heads, hd)
+    q, k, v = (q5[:, :, i].transpose(1, 2).contiguous() for i in range(3))
+    ctx = attention_core(q, k, v, hd ** -0.5, causal)              # fp32 math
+    ctx16 = ctx.transpose(1, 2).reshape(B * S, d).to(torch.float16)
+    sel = ctx16 if rows is None else ctx16[rows]
+    y, _ = int8_linear(sel.float().numpy(), pk["out_w"], pk["out_s"], pk["out_b"])
+    return {"qkv16": qkv16, "ctx16": ctx16, "out": torch.from_numpy(y)}

@@ -1,0 +1,117 @@
+"""C-ABI checks that need no GPU: the library loads, exports every symbol the header declares,
+and rejects invalid arguments with its documented negative status codes before touching the
+device (every call below fails argument validation, so no kernel is launched)."""
+import ctypes as C
+import re
+from pathlib import Path
+
+import pytest
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "mi355attn.h"
+
+
+def _lib():
+    from tiktok_techjam_2026_track3_amd import _lib
+    return _lib
+
+
+def _declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(mi355_\w+)\s*\(", text)))
+
+
+def _status_codes():
+    return {m.group(1): int(m.group(2))
+            for m in re.finditer(r"#define\s+(MI355_\w+)\s+\(?(-?\d+)\)?", HEADER.read_text())}
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib()
+    h = L.lib()
+    declared = _declared_functions()
+    assert declared, "no declarations parsed"
+    for name in declared:
+        assert hasattr(h, name), f"{name} declared in {HEADER.name} but not exported"
+    assert set(declared) == set(L.EXPORTED), "ctypes signature table out of sync with the header"
+
+
+def test_version_and_status_strings():
+    L = _lib()
+    assert L.lib().mi355_version() >= 100
+    codes = _status_codes()
+    for name, code in codes.items():
+        if name.startswith("MI355_E_"):
+            msg = L.status_string(code)
+            assert msg and msg != "unknown status", name
+
+
+def test_dtype_codes_match_header():
+    import torch
+    L = _lib()
+    codes = _status_codes()
+    assert L.dtype_code(torch.float32) == codes["MI355_F32"]
+    assert L.dtype_code(torch.float16) == codes["MI355_F16"]
+    assert L.dtype_code(torch.bfloat16) == codes["MI355_BF16"]
+    with pytest.raises(TypeError):
+        L.dtype_code(torch.int32)
+
+
+def test_gemm_argument_validation():
+    L = _lib()
+    h = L.lib()
+    codes = _status_codes()
+    fake = 1 << 20                                   # aligned, never dereferenced
+    assert h.mi355_gemm_bias(1, 1, fake, 64, fake, 64, None, fake, 64, -1, 64, 64, None, None) == codes["MI355_E_BAD_SIZE"]
+    assert h.mi355_gemm_bias(1, 1, None, 64, fake, 64, None, fake, 64, 4, 64, 64, None, None) == codes["MI355_E_NULL_POINTER"]
+    assert h.mi355_gemm_bias(7, 1, fake, 64, fake, 64, None, fake, 64, 4, 64, 64, None, None) == codes["MI355_E_BAD_DTYPE"]
+    assert h.mi355_gemm_bias(1, 1, fake, 64, fake, 64, None, fake, 64, 4, 64, 60, None, None) == codes["MI355_E_ALIGNMENT"]
+    assert h.mi355_gemm_bias(1, 1, fake + 2, 64, fake, 64, None, fake, 64, 4, 64, 64, None, None) == codes["MI355_E_ALIGNMENT"]
+    assert h.mi355_gemm_bias(0, 1, fake, 64, fake, 64, None, fake, 64, 4, 64, 64, None, None) == codes["MI355_E_UNSUPPORTED"]
+    assert h.mi355_gemm_bias(1, 1, fake, 32, fake, 64, None, fake, 64, 4, 64, 64, None, None) == codes["MI355_E_BAD_SIZE"]
+    # empty problems are a successful no-op
+    assert h.mi355_gemm_bias(1, 1, None, 64, None, 64, None, None, 64, 0, 64, 64, None, None) == 0
+
+
+def test_attention_argument_validation():
+    L = _lib()
+    h = L.lib()
+    codes = _status_codes()
+    fake = 1 << 20
+    st = L.i64_array((3 * 64 * 4 * 16, 3 * 64 * 4, 64))
+    ost = L.i64_array((64 * 4 * 16, 64 * 4, 64))
+
+    def call(dtype=1, hd=64, B=2, S=16, q=fake, scale=0.125, strides=st):
+        return h.mi355_attn_fwd(dtype, q, fake, fake, fake, B, 4, S, S, hd, strides, strides,
+                                strides, ost, scale, 0, None, 0, None)
+
+    assert call(hd=96) == codes["MI355_E_HEAD_DIM"]
+    assert call(hd=256) == codes["MI355_E_HEAD_DIM"]
+    assert call(dtype=5) == codes["MI355_E_BAD_DTYPE"]
+    assert call(q=None) == codes["MI355_E_NULL_POINTER"]
+    assert call(q=fake + 8) == codes["MI355_E_ALIGNMENT"]
+    assert call(scale=0.0) == codes["MI355_E_UNSUPPORTED"]
+    assert call(B=-1) == codes["MI355_E_BAD_SIZE"]
+    assert call(strides=L.i64_array((3, 64, 64))) == codes["MI355_E_ALIGNMENT"]
+    assert call(B=0) == 0
+
+
+def test_int8_argument_validation():
+    L = _lib()
+    h = L.lib()
+    codes = _status_codes()
+    fake = 1 << 20
+    assert h.mi355_quant_rows_i8(1, fake, 64, fake, fake, 4, 60, 0, None) == codes["MI355_E_ALIGNMENT"]
+    assert h.mi355_quant_rows_i8(1, fake, 64, fake, fake, 4, 64, 2, None) == codes["MI355_E_UNSUPPORTED"]
+    assert h.mi355_quant_rows_i8(1, None, 64, fake, fake, 4, 64, 0, None) == codes["MI355_E_NULL_POINTER"]
+    assert h.mi355_gemm_i8(fake, fake, fake, fake, None, 1, fake, 64, None, 4, 64, 40, None, None) == codes["MI355_E_ALIGNMENT"]
+    assert h.mi355_gemm_i8(fake, fake, None, fake, None, 1, fake, 64, None, 4, 64, 64, None, None) == codes["MI355_E_NULL_POINTER"]
+    assert h.mi355_gemm_i8(fake, fake, fake, fake, None, 9, fake, 64, None, 4, 64, 64, None, None) == codes["MI355_E_BAD_DTYPE"]
+
+
+def test_kernel_error_carries_status():
+    L = _lib()
+    with pytest.raises(L.KernelError) as ei:
+        L.check("mi355_attn_fwd", -5)
+    assert ei.value.status == -5 and "head_dim" in str(ei.value)

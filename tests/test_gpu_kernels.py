@@ -1,0 +1,228 @@
+"""GPU parity of each kernel against the CPU oracle, through the C-ABI (ops wrappers).
+
+Floating-point kernels are checked against an fp64 evaluation of the same (already rounded)
+inputs with an explicit error bound built from the rounding points of the kernel:
+  GEMM:      |out - ref| <= u_out*|ref| + 4*K*2^-24 * (|A|·|W|^T) + 1e-7
+  attention: |out - ref| <= (2*u_p + 2^-18) * (P·|V|) + u_out*|ref| + 1e-7
+where u = 2^-11 (fp16), 2^-8 (bf16), 2^-24 (fp32) is the unit round-off of the type the value is
+rounded to (probabilities P for u_p, the stored output for u_out). The int8 kernels are
+compared bit for bit.
+"""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import int8 as OI
+
+pytestmark = pytest.mark.gpu
+
+UNIT = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8, torch.float32: 2.0 ** -24}
+
+
+def _ops():
+    from tiktok_techjam_2026_track3_amd import ops
+    return ops
+
+
+def _rand(shape, dtype, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(*shape, generator=g) * scale).to(dtype)
+
+
+def _report(name, err, bound):
+    worst = float((err / bound).max())
+    print(f"{name}: max_err={float(err.max()):.3g} worst err/bound={worst:.3f}", flush=True)
+    return worst
+
+
+# --------------------------------------------------------------------------------- GEMM
+GEMM_SHAPES = [(1, 64, 64), (128, 768, 256), (300, 200, 136), (513, 130, 1024), (2048, 3072, 1024),
+               (1000, 1536, 512)]
+
+
+@pytest.mark.parametrize("dtype,out_dtype", [(torch.float16, torch.float16),
+                                             (torch.bfloat16, torch.bfloat16),
+                                             (torch.float32, torch.float32),
+                                             (torch.bfloat16, torch.float16),
+                                             (torch.float16, torch.bfloat16)])
+@pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
+def test_linear_error_bound(gpu, dtype, out_dtype, M, N, K):
+    ops = _ops()
+    a = _rand((M, K), dtype, 1)
+    w = _rand((N, K), dtype, 2, scale=K ** -0.5)
+    b = _rand((N,), torch.float32, 3, scale=0.1)
+    print(f"linear dtype={dtype} out={out_dtype} M={M} N={N} K={K}", flush=True)
+    out = ops.linear(a.to(gpu), w.to(gpu), b.to(gpu), out_dtype=out_dtype)
+    assert out.dtype == out_dtype
+    out = out.cpu().double()
+    a64, w64, b64 = a.double(), w.double(), b.double()
+    ref = a64 @ w64.T + b64
+    bound = UNIT[out_dtype] * ref.abs() + 4 * K * 2.0 ** -24 * (a64.abs() @ w64.abs().T) + 1e-7
+    err = (out - ref).abs()
+    assert _report("linear", err, bound) <= 1.0
+
+
+def test_linear_strided_input_and_row_mask(gpu):
+    ops = _ops()
+    M, N, K = 200, 96, 64
+    big = _rand((M, 3 * K), torch.float16, 4)
+    x = big[:, K:2 * K]                        # row stride 3K, unit column stride
+    w = _rand((N, K), torch.float16, 5, scale=0.125)
+    b = _rand((N,), torch.float32, 6)
+    rows = torch.rand(M, generator=torch.Generator().manual_seed(7)) > 0.3
+    out = ops.linear(big.to(gpu)[:, K:2 * K], w.to(gpu), b.to(gpu), row_valid=rows.to(gpu)).cpu()
+    ref = x.double() @ w.double().T + b.double()
+    assert torch.all(out[~rows] == 0)
+    bound = UNIT[torch.float16] * ref.abs() + 4 * K * 2.0 ** -24 * (x.double().abs() @ w.double().abs().T) + 1e-7
+    assert ((out.double() - ref).abs()[rows] <= bound[rows]).all()
+
+
+def test_linear_rejects_bad_arguments(gpu):
+    ops = _ops()
+    from tiktok_techjam_2026_track3_amd._lib import KernelError
+    a = torch.zeros(4, 12, device=gpu, dtype=torch.float16)   # K=12 is not a multiple of 8
+    w = torch.zeros(8, 12, device=gpu, dtype=torch.float16)
+    with pytest.raises(KernelError):
+        ops.linear(a, w)
+    with pytest.raises(ValueError):
+        ops.linear(a, torch.zeros(8, 16, device=gpu, dtype=torch.float16))
+
+
+# ---------------------------------------------------------------------------- attention
+def _attn_check(gpu, dtype, B, H, Sq, Sk, hd, causal, key_valid=None, packed=False, seed=0, qscale=1.0):
+    ops = _ops()
+    print(f"attention dtype={dtype} B={B} H={H} Sq={Sq} Sk={Sk} hd={hd} causal={causal} "
+          f"mask={key_valid is not None} packed={packed}", flush=True)
+    if packed:
+        assert Sq == Sk
+        qkv = _rand((B, Sq, 3, H, hd), dtype, seed)
+        qkv[:, :, 0] = (qkv[:, :, 0].float() * qscale).to(dtype)
+        g_qkv = qkv.to(gpu)
+        q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+        gq, gk, gv = g_qkv[:, :, 0], g_qkv[:, :, 1], g_qkv[:, :, 2]
+    else:
+        q = _rand((B, Sq, H, hd), dtype, seed, scale=qscale)
+        k = _rand((B, Sk, H, hd), dtype, seed + 1)
+        v = _rand((B, Sk, H, hd), dtype, seed + 2)
+        gq, gk, gv = q.to(gpu), k.to(gpu), v.to(gpu)
+    kv = None if key_valid is None else key_valid.to(gpu)
+    out = ops.attention(gq, gk, gv, scale=hd ** -0.5, causal=causal, key_valid=kv).cpu().double()
+    tq, tk, tv = (t.double().transpose(1, 2) for t in (q, k, v))
+    ref = OA.attention_core(tq, tk, tv, hd ** -0.5, causal, key_valid).transpose(1, 2)
+    pav = OA.attention_core(tq, tk, tv.abs(), hd ** -0.5, causal, key_valid).transpose(1, 2)
+    up = UNIT[dtype] if dtype != torch.float32 else 2.0 ** -22
+    bound = (2 * up + 2.0 ** -18) * pav + UNIT[dtype] * ref.abs() + 1e-7
+    finite = torch.isfinite(ref)
+    assert torch.equal(torch.isfinite(out), finite)
+    err = (out - ref).abs()[finite]
+    assert _report("attention", err, bound[finite]) <= 1.0
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("S", [1, 63, 128, 200, 1000])
+def test_attention_16bit(gpu, dtype, hd, causal, S):
+    _attn_check(gpu, dtype, 2, 3, S, S, hd, causal)
+
+
+@pytest.mark.parametrize("hd", [64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("S", [1, 50, 128, 300])
+def test_attention_fp32(gpu, hd, causal, S):
+    _attn_check(gpu, torch.float32, 2, 2, S, S, hd, causal)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_packed_qkv_views(gpu, dtype, causal):
+    _attn_check(gpu, dtype, 2, 4, 333, 333, 64, causal, packed=True, seed=11)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_attention_rectangular_and_large_scores(gpu, dtype):
+    _attn_check(gpu, dtype, 1, 2, 100, 700, 64, False, seed=21)
+    # large logits exercise the lazy max update (tile maxima grow by more than the threshold)
+    _attn_check(gpu, dtype, 1, 2, 256, 640, 64, False, seed=22, qscale=6.0)
+    _attn_check(gpu, dtype, 1, 2, 256, 256, 64, True, seed=23, qscale=6.0)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_key_mask(gpu, dtype, causal):
+    B, S = 3, 150
+    g = torch.Generator().manual_seed(5)
+    mask = torch.rand(B, S, generator=g) > 0.25
+    mask[:, 0] = True                         # every causal row keeps at least key 0
+    mask[2] = torch.arange(S) < 77            # a prefix mask (the benchmark's padding form)
+    _attn_check(gpu, dtype, B, 2, S, S, 64, causal, key_valid=mask, seed=31)
+
+
+def test_attention_fully_masked_batch_gives_nan(gpu):
+    ops = _ops()
+    q = torch.randn(2, 70, 1, 64, dtype=torch.float16, device=gpu)
+    mask = torch.ones(2, 70, dtype=torch.bool, device=gpu)
+    mask[1] = False
+    out = ops.attention(q, q, q, key_valid=mask).cpu()
+    assert torch.isfinite(out[0]).all() and torch.isnan(out[1]).all()
+
+
+def test_attention_rejects_unsupported_head_dim(gpu):
+    ops = _ops()
+    from tiktok_techjam_2026_track3_amd._lib import KernelError
+    q = torch.zeros(1, 8, 1, 96, dtype=torch.float16, device=gpu)
+    with pytest.raises(KernelError, match="head_dim"):
+        ops.attention(q, q, q)
+
+
+# --------------------------------------------------------------------------------- int8
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("mode", [0, 1])
+def test_quant_rows_bit_exact(gpu, dtype, mode):
+    ops = _ops()
+    x = _rand((300, 4096), dtype, 41, scale=0.7)
+    x[3] = 0                                   # zero row exercises the clamp
+    x[4, :16] = torch.tensor([2.5, -2.5, 0.5, 1.5] * 4, dtype=dtype)
+    q, s = ops.quant_rows_i8(x.to(gpu), mode=mode)
+    if mode == 0:
+        wq, ws = OI.quant_rows(x.float().numpy())
+    else:
+        wq, ws = OI.quant_weight(x.float().numpy())
+    np.testing.assert_array_equal(s.cpu().numpy(), ws)
+    np.testing.assert_array_equal(q.cpu().numpy(), wq)
+
+
+@pytest.mark.parametrize("M,N,K", [(1, 32, 16), (257, 300, 512), (1024, 1536, 4096), (4096, 4096, 4096)])
+def test_gemm_i8_accumulators_bit_exact(gpu, M, N, K):
+    ops = _ops()
+    rng = np.random.default_rng(M + N + K)
+    a = rng.integers(-128, 128, size=(M, K), dtype=np.int8)
+    w = rng.integers(-128, 128, size=(N, K), dtype=np.int8)
+    a[0, :] = -128
+    w[0, :] = -128                             # extreme accumulator K * 128^2
+    acc = torch.empty(M, N, dtype=torch.int32, device=gpu)
+    ga, gw = torch.from_numpy(a).to(gpu), torch.from_numpy(w).to(gpu)
+    ones_a = torch.ones(M, device=gpu)
+    ones_w = torch.ones(N, device=gpu)
+    ops.linear_i8(ga, gw, ones_a, ones_w, acc_out=acc, want_out=False)
+    np.testing.assert_array_equal(acc.cpu().numpy(), OI.int8_gemm(a, w))
+
+
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32, torch.bfloat16])
+def test_gemm_i8_dequant_bit_exact(gpu, out_dtype):
+    ops = _ops()
+    M, N, K = 300, 520, 1024
+    h = _rand((M, K), torch.float32, 51)
+    w = _rand((N, K), torch.float32, 52, scale=0.02)
+    bias = _rand((N,), torch.float32, 53, scale=0.03)
+    a8, sa = OI.quant_rows(h.numpy())
+    w8, sw = OI.quant_weight(w.numpy())
+    want32, _ = OI.int8_linear(h.numpy(), w8, sw, bias.numpy())
+    out = ops.linear_i8(torch.from_numpy(a8).to(gpu), torch.from_numpy(w8).to(gpu),
+                        torch.from_numpy(sa).to(gpu), torch.from_numpy(sw).to(gpu), bias.to(gpu),
+                        out_dtype=out_dtype).cpu()
+    want = torch.from_numpy(want32).to(out_dtype)
+    assert torch.equal(out, want)

@@ -1,0 +1,97 @@
+"""Module and plugin mechanics that need no GPU (mirrors the reference's SubmissionRuntimeTests,
+Project/tools/tests/evidence_submission_test.py:729-811, minus the CPU compute route: this
+build has no CPU path, so a CPU forward must raise instead of silently running torch)."""
+import pytest
+import torch
+
+from oracle import model as OM
+from tiktok_techjam_2026_track3_amd import (BaselineSelfAttention, Int8SelfAttention, SelfAttention,
+                                            build, make_user_optimized_transformer, swap_attention)
+from tiktok_techjam_2026_track3_amd import workloads as W
+
+
+def test_same_attributes_and_state_dict_as_reference_module():
+    torch.manual_seed(0)
+    ref = OM.BaselineSelfAttention(64, 4)
+    mine = SelfAttention(64, 4)
+    assert list(ref.state_dict().keys()) == list(mine.state_dict().keys())
+    for a in ("d_model", "num_heads", "head_dim", "scale"):
+        assert getattr(ref, a) == getattr(mine, a)
+    res = mine.load_state_dict(ref.state_dict(), strict=True)
+    assert not res.missing_keys and not res.unexpected_keys
+    assert BaselineSelfAttention is SelfAttention
+    with pytest.raises(ValueError):
+        SelfAttention(65, 4)
+
+
+def test_cpu_forward_raises_instead_of_falling_back():
+    mod = SelfAttention(32, 4)
+    with pytest.raises(RuntimeError, match="no CPU path"):
+        mod(torch.randn(1, 8, 32))
+    with pytest.raises(ValueError):
+        mod(torch.randn(1, 8, 16))
+
+
+def test_load_state_dict_and_apply_drop_derived_caches():
+    mod = SelfAttention(32, 4)
+    mod.__dict__["_mi355_pack"] = object()
+    mod.__dict__["_mi355_mask"] = object()
+    mod.load_state_dict(mod.state_dict(), strict=True)
+    assert "_mi355_pack" not in mod.__dict__ and "_mi355_mask" not in mod.__dict__
+    mod.__dict__["_mi355_pack"] = object()
+    mod.half()
+    assert "_mi355_pack" not in mod.__dict__
+
+
+def test_param_stamp_tracks_in_place_updates():
+    mod = SelfAttention(32, 4)
+    s1 = mod._param_stamp()
+    with torch.no_grad():
+        mod.q_proj.weight.mul_(2)
+    assert mod._param_stamp() != s1
+
+
+def test_core_dtype_policy():
+    mod = SelfAttention(32, 4)
+    assert mod.core_dtype(torch.float16) == torch.float16
+    assert mod.core_dtype(torch.float32) == torch.float32
+    assert mod.core_dtype(torch.bfloat16) == torch.float16
+
+
+def test_plugin_build_and_swap_keep_state_dict_keys():
+    cfg = OM.TransformerConfig(batch_size=2, seq_len=8, d_model=16, num_heads=4, ffn_dim=16,
+                               num_layers=2, causal=True)
+    torch.manual_seed(7)
+    base = OM.BaselineTransformer(cfg)
+    cand = build(OM, cfg)
+    assert isinstance(cand, OM.UserOptimizedTransformer)
+    assert all(type(l.attention) is SelfAttention for l in cand.layers)
+    res = cand.load_state_dict(base.state_dict(), strict=True)
+    assert not res.missing_keys and not res.unexpected_keys
+    # class-swap idiom (k001_sdpa.py:55-61): parameters are the same objects afterwards
+    params_before = [id(p) for p in base.parameters()]
+    assert swap_attention(base, int8=True) == 2
+    assert [id(p) for p in base.parameters()] == params_before
+    assert all(type(l.attention) is Int8SelfAttention for l in base.layers)
+    Uot = make_user_optimized_transformer(OM)
+    m = Uot(cfg)
+    assert issubclass(Uot, OM.BaselineTransformer)
+    assert all(type(l.attention) is SelfAttention for l in m.layers)
+
+
+def test_workload_accounting():
+    c2 = W.CONFIGS["C2"]
+    f = c2.flops()
+    assert f["qkv"] == 2 * 16384 * 1024 * 3072
+    assert f["attn"] == 4 * 8 * 16 * 2048 ** 2 * 64
+    c3 = W.CONFIGS["C3"]
+    assert c3.flops()["attn"] == 4 * 4 * 32 * 8192 ** 2 * 64 / 2
+    assert W.CONFIGS["C5"].flops()["attn"] == pytest.approx(655_360e9)
+    p = W.make_params(W.CONFIGS["C1"])
+    assert set(p) == {f"{n}.{t}" for n in W.PROJECTIONS for t in ("weight", "bias")}
+    assert abs(p["q_proj.weight"].std().item() - 256 ** -0.5) < 0.01
+    x1 = W.make_input(W.CONFIGS["C1"], 1234)
+    x2 = W.make_input(W.CONFIGS["C1"], 1234)
+    assert torch.equal(x1, x2) and x1.dtype == torch.float32
+    # inputs and weights come from different streams
+    assert not torch.allclose(x1[0, :256].reshape(-1)[:100], p["q_proj.weight"].reshape(-1)[:100] * 16)

@@ -1,0 +1,19 @@
+"""MI355X-native (gfx950) attention-block hot path of the TechJam 2026 Track 3 transformer.
+
+Public API:
+  SelfAttention, Int8SelfAttention      drop-in modules for BaselineSelfAttention
+  build, swap_attention,
+  make_user_optimized_transformer       the reference's plugin insertion points
+  ops                                   torch wrappers of the C-ABI kernels
+  workloads                             the measured configurations and seeded inputs
+"""
+from .attention import Int8SelfAttention, SelfAttention
+from .plugin import build, make_user_optimized_transformer, swap_attention
+from . import ops, workloads
+
+BaselineSelfAttention = SelfAttention  # the reference's class name
+
+__all__ = [
+    "SelfAttention", "Int8SelfAttention", "BaselineSelfAttention", "build", "swap_attention",
+    "make_user_optimized_transformer", "ops", "workloads",
+]

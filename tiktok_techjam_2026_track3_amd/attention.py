@@ -1,0 +1,235 @@
+"""Drop-in attention modules backed by the gfx950 kernels of libmi355attn.so.
+
+``SelfAttention`` mirrors ``BaselineSelfAttention`` (torch_transformer_benchmark.py:59-122):
+same constructor, attributes (d_model, num_heads, head_dim, scale, q_proj, k_proj, v_proj,
+out_proj), state-dict keys and ``forward(x, valid_token_mask=None, causal=False)`` contract.
+A GPU forward is three launches on the current stream:
+
+  1. packed QKV projection  x[T, d] · W_qkv[3d, d]^T + b_qkv -> qkv[T, 3d]
+     (the packing of Project/submission/dispatcher_region.py:789-792);
+  2. streamed attention reading q/k/v as strided views of qkv (no head-split copy, as in
+     dispatcher_region.py:1026-1029) and writing ctx in [B, S, H, hd] = [T, d] order (the free
+     head merge of dispatcher_region.py:314-317);
+  3. output projection ctx · W_o^T + b_o with the output-row mask fused in its epilogue.
+
+``Int8SelfAttention`` is the W8A8 variant of Project/kernels/k008_int8_gemm.py:148-235:
+per-token int8 activations, per-output-channel int8 weights, exact int32 accumulation, fp32
+dequantisation, fp16 SDPA.
+
+Precision policy: fp32 inputs run fp32 end to end; fp16 inputs run fp16 storage with fp32
+accumulation; bf16 inputs run the QKV projection on bf16 operands but store q/k/v, the
+probabilities and the context in fp16 (``bf16_core_dtype``), whose 3 extra mantissa bits keep
+the block within the elementwise 2e-3 / 2e-2 tolerance of fp32 math that a bf16-stored core
+misses; the output is bf16. Values beyond the fp16 range (65504) in q/k/v or the context become
+inf and surface as non-finite outputs; set ``bf16_core_dtype = torch.bfloat16`` for such models.
+
+There is no CPU or eager-torch fallback: CPU inputs raise, and a missing library raises.
+Derived caches (packed / quantised weights) live in the instance ``__dict__`` and are dropped
+on ``load_state_dict`` and ``_apply`` (the contract of dispatcher_region.py:809-836), and are
+also re-derived whenever a parameter's storage or version counter changes.
+"""
+from __future__ import annotations
+
+from typing import Callable, Optional, Tuple
+
+import torch
+import torch.nn as nn
+
+from . import ops
+
+_CACHE_KEYS = ("_mi355_pack", "_mi355_mask")
+
+
+class SelfAttention(nn.Module):
+    """Multi-head self-attention with the reference's module API, on gfx950 kernels."""
+
+    bf16_core_dtype = torch.float16
+
+    def __init__(self, d_model: int, num_heads: int) -> None:
+        super().__init__()
+        if d_model % num_heads != 0:
+            raise ValueError("d_model must be divisible by num_heads")
+        self.d_model = d_model
+        self.num_heads = num_heads
+        self.head_dim = d_model // num_heads
+        self.scale = self.head_dim ** -0.5
+        self.q_proj = nn.Linear(d_model, d_model, bias=True)
+        self.k_proj = nn.Linear(d_model, d_model, bias=True)
+        self.v_proj = nn.Linear(d_model, d_model, bias=True)
+        self.out_proj = nn.Linear(d_model, d_model, bias=True)
+
+    # ----------------------------------------------------------------------------- caches
+    def invalidate_caches(self) -> None:
+        for key in _CACHE_KEYS:
+            self.__dict__.pop(key, None)
+
+    def load_state_dict(self, *args, **kwargs):
+        result = super().load_state_dict(*args, **kwargs)
+        self.invalidate_caches()
+        return result
+
+    def _apply(self, fn, recurse=True):
+        result = super()._apply(fn, recurse=recurse)
+        self.invalidate_caches()
+        return result
+
+    def _param_stamp(self) -> Tuple:
+        stamp = []
+        for lin in (self.q_proj, self.k_proj, self.v_proj, self.out_proj):
+            for p in (lin.weight, lin.bias):
+                stamp.append((p.data_ptr(), p._version, p.dtype, p.device))
+        return tuple(stamp)
+
+    def _cached(self, key, build):
+        entry = self.__dict__.get("_mi355_pack")
+        if entry is not None and entry[0] == key:
+            return entry[1]
+        value = build()
+        self.__dict__["_mi355_pack"] = (key, value)
+        return value
+
+    def core_dtype(self, dtype: torch.dtype) -> torch.dtype:
+        """Storage dtype of q/k/v, probabilities and context for input dtype ``dtype``."""
+        return self.bf16_core_dtype if dtype == torch.bfloat16 else dtype
+
+    def _packed_weights(self, dtype: torch.dtype, device: torch.device):
+        """(W_qkv [3d, d] in the input dtype, b_qkv fp32, W_o [d, d] in the core dtype, b_o fp32)."""
+        core = self.core_dtype(dtype)
+
+        def build():
+            with torch.no_grad():
+                w_qkv = torch.cat([self.q_proj.weight, self.k_proj.weight, self.v_proj.weight], 0)
+                b_qkv = torch.cat([self.q_proj.bias, self.k_proj.bias, self.v_proj.bias], 0)
+                f32 = torch.float32
+                return (w_qkv.to(device=device, dtype=dtype).contiguous(),
+                        b_qkv.to(device=device, dtype=f32).contiguous(),
+                        self.out_proj.weight.to(device=device, dtype=core).contiguous(),
+                        self.out_proj.bias.to(device=device, dtype=f32).contiguous())
+        return self._cached(("fp", dtype, core, device, self._param_stamp()), build)
+
+    # ------------------------------------------------------------------------------- masks
+    def _resolve_mask(self, mask: Optional[torch.Tensor], B: int, S: int, device: torch.device):
+        """Returns (key_valid [B,S] bool or None, row_valid [B*S] bool or None).
+
+        An all-true mask is dropped (its masked_fill calls are identities); deciding that needs
+        one host sync per distinct mask tensor, cached by identity and version as the
+        reference's dispatcher does (dispatcher_region.py:1102-1146).
+        """
+        if mask is None:
+            return None, None
+        if mask.dtype != torch.bool or tuple(mask.shape) != (B, S):
+            raise ValueError(f"valid_token_mask must be a bool tensor of shape ({B}, {S})")
+        if mask.device != device:
+            raise ValueError("valid_token_mask must be on the input's device")
+        stamp = (id(mask), mask.data_ptr(), mask._version)
+        cached = self.__dict__.get("_mi355_mask")
+        if cached is not None and cached[0] == stamp:
+            all_true = cached[1]
+        else:
+            all_true = bool(mask.all().item())
+            self.__dict__["_mi355_mask"] = (stamp, all_true)
+        if all_true:
+            return None, None
+        m = mask.contiguous()
+        return m, m.view(B * S)
+
+    # ----------------------------------------------------------------------------- forward
+    def _check_input(self, x: torch.Tensor) -> Tuple[int, int]:
+        if x.dim() != 3 or x.shape[-1] != self.d_model:
+            raise ValueError(f"expected x of shape [B, S, {self.d_model}], got {tuple(x.shape)}")
+        if x.device.type != "cuda":
+            raise RuntimeError("SelfAttention runs only on the GPU kernels; got a "
+                               f"{x.device.type} tensor (there is no CPU path)")
+        if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            raise TypeError(f"unsupported dtype {x.dtype}")
+        return x.shape[0], x.shape[1]
+
+    def _qkv_views(self, qkv: torch.Tensor, B: int, S: int):
+        qkv5 = qkv.view(B, S, 3, self.num_heads, self.head_dim)
+        return qkv5[:, :, 0], qkv5[:, :, 1], qkv5[:, :, 2]
+
+    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,
+                causal: bool = False) -> torch.Tensor:
+        return self.run(x, valid_token_mask, causal)
+
+    def run(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,
+            causal: bool = False, keep: Optional[dict] = None,
+            marks: Optional[Callable[[str], None]] = None) -> torch.Tensor:
+        """The forward pass.
+
+        ``keep`` (a dict) receives the qkv and ctx intermediates; ``marks(stage)`` is called
+        before each kernel launch ("qkv", "attn", "out") and after the last ("end"), so a caller
+        can bracket every kernel with events on the launch stream.
+        """
+        mark = marks or (lambda _stage: None)
+        B, S = self._check_input(x)
+        d = self.d_model
+        key_valid, row_valid = self._resolve_mask(valid_token_mask, B, S, x.device)
+        w_qkv, b_qkv, w_o, b_o = self._packed_weights(x.dtype, x.device)
+        core = self.core_dtype(x.dtype)
+        x2 = x.reshape(B * S, d)
+        if x2.stride(1) != 1:
+            x2 = x2.contiguous()
+        mark("qkv")
+        qkv = ops.linear(x2, w_qkv, b_qkv, out_dtype=core)
+        q, k, v = self._qkv_views(qkv, B, S)
+        mark("attn")
+        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid)
+        mark("out")
+        out = ops.linear(ctx.view(B * S, d), w_o, b_o, row_valid=row_valid, out_dtype=x.dtype)
+        mark("end")
+        if keep is not None:
+            keep.update(qkv=qkv, ctx=ctx)
+        return out.view(B, S, d)
+
+
+class Int8SelfAttention(SelfAttention):
+    """W8A8 variant: int8 projections with exact int32 accumulation, fp16 SDPA.
+
+    Mirrors the attention half of ``block_forward`` in Project/kernels/k008_int8_gemm.py:189-223:
+    qkv = fp16(int8_linear(x)) -> fp16 attention -> int8_linear(ctx). The output dtype is the
+    input dtype.
+    """
+
+    def _int8_weights(self, device: torch.device):
+        def build():
+            with torch.no_grad():
+                w_qkv = torch.cat([self.q_proj.weight, self.k_proj.weight, self.v_proj.weight], 0)
+                b_qkv = torch.cat([self.q_proj.bias, self.k_proj.bias, self.v_proj.bias], 0)
+                w_qkv = w_qkv.to(device=device, dtype=torch.float32).contiguous()
+                w_o = self.out_proj.weight.to(device=device, dtype=torch.float32).contiguous()
+                wq_i8, s_qkv = ops.quant_rows_i8(w_qkv, mode=1)
+                wo_i8, s_o = ops.quant_rows_i8(w_o, mode=1)
+                return (wq_i8, s_qkv, b_qkv.to(device=device, dtype=torch.float32).contiguous(),
+                        wo_i8, s_o,
+                        self.out_proj.bias.to(device=device, dtype=torch.float32).contiguous())
+        return self._cached(("i8", device, self._param_stamp()), build)
+
+    def run(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,
+            causal: bool = False, keep: Optional[dict] = None,
+            marks: Optional[Callable[[str], None]] = None) -> torch.Tensor:
+        mark = marks or (lambda _stage: None)
+        B, S = self._check_input(x)
+        d = self.d_model
+        if d % 16:
+            raise ValueError("the int8 path needs d_model % 16 == 0")
+        key_valid, row_valid = self._resolve_mask(valid_token_mask, B, S, x.device)
+        wq, s_qkv, b_qkv, wo, s_o, b_o = self._int8_weights(x.device)
+        x2 = x.reshape(B * S, d)
+        if x2.stride(1) != 1:
+            x2 = x2.contiguous()
+        mark("quant_x")
+        xq, sx = ops.quant_rows_i8(x2, mode=0)
+        mark("qkv")
+        qkv = ops.linear_i8(xq, wq, sx, s_qkv, b_qkv, out_dtype=torch.float16)
+        q, k, v = self._qkv_views(qkv, B, S)
+        mark("attn")
+        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid)
+        mark("quant_ctx")
+        cq, sc = ops.quant_rows_i8(ctx.view(B * S, d), mode=0)
+        mark("out")
+        out = ops.linear_i8(cq, wo, sc, s_o, b_o, out_dtype=x.dtype, row_valid=row_valid)
+        mark("end")
+        if keep is not None:
+            keep.update(qkv=qkv, ctx=ctx, x_i8=xq, x_scale=sx, ctx_i8=cq, ctx_scale=sc)
+        return out.view(B, S, d)

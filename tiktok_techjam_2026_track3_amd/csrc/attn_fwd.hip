@@ -1,0 +1,430 @@
+// Streamed scaled-dot-product attention forward (online softmax) for gfx950.
+//
+// fp16 / bf16 kernel (MFMA):
+//   * one work-group = NW waves = NW*32 queries of one (batch, head); each wave owns 32 queries;
+//   * K and V are streamed in tiles of 64 keys through double-buffered LDS;
+//   * scores are produced transposed, S^T = K · Q^T (32x32x16 MFMA: A = K rows from LDS,
+//     B = Q^T kept in registers), so each lane holds 32 scores of ONE query: the row max needs
+//     one lane-pair exchange (v_permlane32_swap) per tile and the row sum none until the end;
+//   * probabilities are exp2(s*scale*log2e - m*scale*log2e) in fp32, rounded to the input dtype
+//     (the rounding point of torch_transformer_benchmark.py:111) and fed straight from registers
+//     as the B operand of O^T += V^T · P^T; V^T comes from an LDS tile that the loader writes
+//     transposed, with keys permuted inside 16-key groups so every A fragment is one 16-byte read;
+//   * the running max is only moved when a tile's max exceeds it by more than 8 (log2 units), so
+//     the O/l rescale is skipped on most tiles; unnormalised probabilities stay <= 2^8;
+//   * causal work-groups stop at the diagonal, mask only tiles that cross it, and are issued
+//     longest-first.
+// fp32 kernel: one query per lane on VALU (the fp32 configuration is launch-latency bound).
+#include "common.h"
+
+namespace {
+
+struct AttnArgs {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;
+  int64_t qs0, qs1, qs2;  // batch, seq, head strides in elements (head_dim stride 1)
+  int64_t ks0, ks1, ks2;
+  int64_t vs0, vs1, vs2;
+  int64_t os0, os1, os2;
+  int64_t B, H, Sq, Sk;
+  float c;    // scale * log2(e)
+  float thr;  // lazy-rescale threshold in raw score units (8 / c)
+  const uint8_t* kv;
+  int64_t kv_sb;
+  int n_qtiles;
+};
+
+constexpr float NEG_INF = -__builtin_huge_valf();
+
+MI355_DEVINL float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Position of key kk (0..63) inside a V^T LDS row: bits 2 and 3 swapped, so the 8 keys a lane
+// group feeds one PV MFMA ({0-3, 8-11} + 4g of each 16-key group) are contiguous.
+MI355_DEVINL int vt_pos(int kk) {
+  return (kk & ~15) | (kk & 3) | (((kk >> 3) & 1) << 2) | (((kk >> 2) & 1) << 3);
+}
+
+template <int NCH>
+MI355_DEVINL int swz(int r) {
+  if constexpr (NCH >= 16)
+    return r & 15;
+  else
+    return (r & 7) ^ ((r >> 3) & 1);
+}
+
+template <typename T>
+MI355_DEVINL typename Mfma<T>::frag pack8(const float* p) {
+  typename Mfma<T>::frag f;
+#pragma unroll
+  for (int r = 0; r < 8; ++r) f[r] = from_f32<T>(p[r]);
+  return f;
+}
+
+template <typename T, int HD, int NW, bool CAUSAL, bool KMASK>
+__global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
+  using MF = Mfma<T>;
+  using frag = typename MF::frag;
+  constexpr int BM = NW * 32;
+  constexpr int BN = 64;
+  constexpr int NT = NW * 64;
+  constexpr int KCH = HD / 8;   // 16-byte chunks per K row
+  constexpr int VCH = BN / 8;   // 16-byte chunks per V^T row
+  constexpr int KS = HD / 16;   // MFMA k-steps of S^T
+  constexpr int MT = HD / 32;   // 32-row tiles of O^T
+  constexpr int K_LOADS = BN * KCH / NT;
+  constexpr int V_UNITS = (BN / 2) * KCH / NT;
+  static_assert(K_LOADS >= 1 && V_UNITS >= 1, "tile/thread shape");
+
+  __shared__ u32x4 k_lds[2][BN * KCH];
+  __shared__ u32x4 vt_lds[2][HD * VCH];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 5, l32 = lane & 31;
+  const int qt = CAUSAL ? (p.n_qtiles - 1 - static_cast<int>(blockIdx.x)) : static_cast<int>(blockIdx.x);
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  const int64_t q_wg = static_cast<int64_t>(qt) * BM;
+  const int64_t qi = q_wg + wave * 32 + l32;
+
+  const T* __restrict__ Qb = static_cast<const T*>(p.q) + b * p.qs0 + h * p.qs2;
+  const T* __restrict__ Kb = static_cast<const T*>(p.k) + b * p.ks0 + h * p.ks2;
+  const T* __restrict__ Vb = static_cast<const T*>(p.v) + b * p.vs0 + h * p.vs2;
+  const uint8_t* __restrict__ kvb = KMASK ? p.kv + b * p.kv_sb : nullptr;
+
+  // Q^T fragments: lane (query qi, slice g) holds Q[qi][16*ks + 8*g .. +7].
+  frag qf[KS];
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    u32x4 v = {0u, 0u, 0u, 0u};
+    if (qi < p.Sq) v = *reinterpret_cast<const u32x4*>(Qb + qi * p.qs1 + 16 * s + 8 * g);
+    qf[s] = __builtin_bit_cast(frag, v);
+  }
+
+  const int64_t kend = CAUSAL ? ((q_wg + BM) < p.Sk ? (q_wg + BM) : p.Sk) : p.Sk;
+  const int n_kt = static_cast<int>((kend + BN - 1) / BN);
+
+  u32x4 rk[K_LOADS], rv0[V_UNITS], rv1[V_UNITS];
+  auto load_global = [&](int j) {
+    const int64_t k0 = static_cast<int64_t>(j) * BN;
+#pragma unroll
+    for (int i = 0; i < K_LOADS; ++i) {
+      const int idx = tid + i * NT, key = idx / KCH, ch = idx % KCH;
+      const int64_t gk = k0 + key;
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (gk < p.Sk) v = *reinterpret_cast<const u32x4*>(Kb + gk * p.ks1 + ch * 8);
+      rk[i] = v;
+    }
+#pragma unroll
+    for (int i = 0; i < V_UNITS; ++i) {
+      const int u = tid + i * NT, pr = u % 32, ch = u / 32;
+      const int64_t gk = k0 + 2 * pr;
+      u32x4 a = {0u, 0u, 0u, 0u}, c = {0u, 0u, 0u, 0u};
+      if (gk < p.Sk) a = *reinterpret_cast<const u32x4*>(Vb + gk * p.vs1 + ch * 8);
+      if (gk + 1 < p.Sk) c = *reinterpret_cast<const u32x4*>(Vb + (gk + 1) * p.vs1 + ch * 8);
+      rv0[i] = a;
+      rv1[i] = c;
+    }
+  };
+  auto store_lds = [&](int s) {
+#pragma unroll
+    for (int i = 0; i < K_LOADS; ++i) {
+      const int idx = tid + i * NT, key = idx / KCH, ch = idx % KCH;
+      k_lds[s][key * KCH + (ch ^ swz<KCH>(key))] = rk[i];
+    }
+    uint32_t* vt32 = reinterpret_cast<uint32_t*>(&vt_lds[s][0]);
+#pragma unroll
+    for (int i = 0; i < V_UNITS; ++i) {
+      const int u = tid + i * NT, pr = u % 32, ch = u / 32;
+      const int pos = vt_pos(2 * pr);
+      const int pch = pos >> 3, pw = (pos & 7) >> 1;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const int row = 8 * ch + e;
+        const uint32_t lo = (rv0[i][e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        const uint32_t hi = (rv1[i][e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        vt32[(row * VCH + (pch ^ swz<VCH>(row))) * 4 + pw] = lo | (hi << 16);
+      }
+    }
+  };
+
+  f32x16 oacc[MT];
+#pragma unroll
+  for (int t = 0; t < MT; ++t)
+#pragma unroll
+    for (int i = 0; i < 16; ++i) oacc[t][i] = 0.f;
+  float m_used = NEG_INF, mu = 0.f, lsum = 0.f;
+
+  if (n_kt > 0) {
+    load_global(0);
+    store_lds(0);
+  }
+  __syncthreads();
+
+  for (int j = 0; j < n_kt; ++j) {
+    const int cur = j & 1;
+    if (j + 1 < n_kt) load_global(j + 1);
+
+    // S^T tile: 64 keys x 32 queries per wave.
+    f32x16 sacc[2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) sacc[t][i] = 0.f;
+      const int krow = 32 * t + l32;
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        const int c = 2 * s + g;
+        const u32x4 a = k_lds[cur][krow * KCH + (c ^ swz<KCH>(krow))];
+        sacc[t] = MF::mma(__builtin_bit_cast(frag, a), qf[s], sacc[t]);
+      }
+    }
+
+    const int64_t k0 = static_cast<int64_t>(j) * BN;
+    const bool need_mask = KMASK || (k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > q_wg);
+    if (need_mask) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int64_t key = k0 + 32 * t + mfma_row(i, lane);
+          bool ok = key < p.Sk;
+          if (CAUSAL) ok = ok && key <= qi;
+          if (KMASK) ok = ok && kvb[key < p.Sk ? key : 0] != 0;
+          if (!ok) sacc[t][i] = NEG_INF;
+        }
+    }
+
+    float mx = NEG_INF;
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[t][i]);
+    mx = pair_max(mx);
+
+    if (__builtin_amdgcn_ballot_w64(mx > m_used + p.thr) != 0) {
+      const float m_new = fmaxf(m_used, mx);
+      const float alpha = (m_used == NEG_INF) ? 0.f : fast_exp2((m_used - m_new) * p.c);
+      lsum *= alpha;
+#pragma unroll
+      for (int t = 0; t < MT; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) oacc[t][i] *= alpha;
+      m_used = m_new;
+      mu = (m_used == NEG_INF) ? 0.f : m_used * p.c;
+    }
+
+    frag pf[2][2];
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      float pv[16];
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        pv[i] = fast_exp2(__builtin_fmaf(sacc[t][i], p.c, -mu));
+        lsum += pv[i];
+      }
+      pf[t][0] = pack8<T>(pv);
+      pf[t][1] = pack8<T>(pv + 8);
+    }
+
+    // O^T (hd x 32 queries) += V^T (hd x 64 keys) . P^T (64 keys x 32 queries)
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      const int vrow = 32 * mt + l32;
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) {
+          const int c = 4 * t + 2 * hh + g;
+          const u32x4 a = vt_lds[cur][vrow * VCH + (c ^ swz<VCH>(vrow))];
+          oacc[mt] = MF::mma(__builtin_bit_cast(frag, a), pf[t][hh], oacc[mt]);
+        }
+    }
+
+    if (j + 1 < n_kt) store_lds(cur ^ 1);
+    __syncthreads();
+  }
+
+  const float ltot = pair_sum(lsum);
+  const float inv = 1.0f / ltot;
+  if (qi < p.Sq) {
+    T* Ob = static_cast<T*>(p.o) + b * p.os0 + qi * p.os1 + h * p.os2;
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int hd0 = 32 * mt + 8 * i4 + 4 * g;
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        t4 w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = from_f32<T>(oacc[mt][4 * i4 + e] * inv);
+        *reinterpret_cast<t4*>(Ob + hd0) = w;
+      }
+  }
+}
+
+// fp32: one query per lane, 64 queries per work-group, K/V tiles of 64 keys in LDS.
+template <int HD, bool CAUSAL, bool KMASK>
+__global__ __launch_bounds__(64) void attn_fwd_f32(AttnArgs p) {
+  constexpr int BN = 64;
+  __shared__ float ks[BN][HD];
+  __shared__ float vs[BN][HD];
+  const int lane = threadIdx.x;
+  const int qt = CAUSAL ? (p.n_qtiles - 1 - static_cast<int>(blockIdx.x)) : static_cast<int>(blockIdx.x);
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  const int64_t q_wg = static_cast<int64_t>(qt) * 64;
+  const int64_t qi = q_wg + lane;
+  const float* Qb = static_cast<const float*>(p.q) + b * p.qs0 + h * p.qs2;
+  const float* Kb = static_cast<const float*>(p.k) + b * p.ks0 + h * p.ks2;
+  const float* Vb = static_cast<const float*>(p.v) + b * p.vs0 + h * p.vs2;
+  const uint8_t* kvb = KMASK ? p.kv + b * p.kv_sb : nullptr;
+
+  float q[HD], acc[HD];
+#pragma unroll
+  for (int d = 0; d < HD; ++d) {
+    q[d] = qi < p.Sq ? Qb[qi * p.qs1 + d] : 0.f;
+    acc[d] = 0.f;
+  }
+  float m = NEG_INF, l = 0.f;
+  const int64_t kend = CAUSAL ? ((q_wg + 64) < p.Sk ? (q_wg + 64) : p.Sk) : p.Sk;
+  for (int64_t k0 = 0; k0 < kend; k0 += BN) {
+    __syncthreads();
+    for (int idx = lane; idx < BN * HD / 4; idx += 64) {
+      const int key = idx / (HD / 4), c4 = idx % (HD / 4);
+      f32x4 kv4 = {0.f, 0.f, 0.f, 0.f}, vv4 = {0.f, 0.f, 0.f, 0.f};
+      if (k0 + key < p.Sk) {
+        kv4 = *reinterpret_cast<const f32x4*>(Kb + (k0 + key) * p.ks1 + 4 * c4);
+        vv4 = *reinterpret_cast<const f32x4*>(Vb + (k0 + key) * p.vs1 + 4 * c4);
+      }
+      *reinterpret_cast<f32x4*>(&ks[key][4 * c4]) = kv4;
+      *reinterpret_cast<f32x4*>(&vs[key][4 * c4]) = vv4;
+    }
+    __syncthreads();
+    for (int kb = 0; kb < BN; kb += 16) {
+      float s[16];
+      float mx = NEG_INF;
+      for (int kk = 0; kk < 16; ++kk) {
+        float d0 = 0.f;
+#pragma unroll
+        for (int d = 0; d < HD; ++d) d0 = __builtin_fmaf(q[d], ks[kb + kk][d], d0);
+        const int64_t key = k0 + kb + kk;
+        bool ok = key < p.Sk;
+        if (CAUSAL) ok = ok && key <= qi;
+        if (KMASK) ok = ok && kvb[key < p.Sk ? key : 0] != 0;
+        s[kk] = ok ? d0 : NEG_INF;
+        mx = fmaxf(mx, s[kk]);
+      }
+      const float m_new = fmaxf(m, mx);
+      const float alpha = (m == NEG_INF) ? 0.f : fast_exp2((m - m_new) * p.c);
+      const float mu = (m_new == NEG_INF) ? 0.f : m_new * p.c;
+      l *= alpha;
+#pragma unroll
+      for (int d = 0; d < HD; ++d) acc[d] *= alpha;
+      for (int kk = 0; kk < 16; ++kk) {
+        const float pk = fast_exp2(__builtin_fmaf(s[kk], p.c, -mu));
+        l += pk;
+#pragma unroll
+        for (int d = 0; d < HD; ++d) acc[d] = __builtin_fmaf(pk, vs[kb + kk][d], acc[d]);
+      }
+      m = m_new;
+    }
+  }
+  if (qi < p.Sq) {
+    float* Ob = static_cast<float*>(p.o) + b * p.os0 + qi * p.os1 + h * p.os2;
+    const float inv = 1.0f / l;
+#pragma unroll
+    for (int d = 0; d < HD; ++d) Ob[d] = acc[d] * inv;
+  }
+}
+
+template <typename T, int HD, int NW>
+int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
+  AttnArgs a = a0;
+  constexpr int BM = NW * 32;
+  a.n_qtiles = static_cast<int>((a.Sq + BM - 1) / BM);
+  dim3 grid(a.n_qtiles, static_cast<unsigned>(a.H), static_cast<unsigned>(a.B));
+  dim3 block(NW * 64);
+  if (causal) {
+    if (kmask) hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, true, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, true, false>), grid, block, 0, s, a);
+  } else {
+    if (kmask) hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, false, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, false, false>), grid, block, 0, s, a);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+template <int HD>
+int launch_f32(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
+  AttnArgs a = a0;
+  a.n_qtiles = static_cast<int>((a.Sq + 63) / 64);
+  dim3 grid(a.n_qtiles, static_cast<unsigned>(a.H), static_cast<unsigned>(a.B));
+  if (causal) {
+    if (kmask) hipLaunchKernelGGL((attn_fwd_f32<HD, true, true>), grid, dim3(64), 0, s, a);
+    else hipLaunchKernelGGL((attn_fwd_f32<HD, true, false>), grid, dim3(64), 0, s, a);
+  } else {
+    if (kmask) hipLaunchKernelGGL((attn_fwd_f32<HD, false, true>), grid, dim3(64), 0, s, a);
+    else hipLaunchKernelGGL((attn_fwd_f32<HD, false, false>), grid, dim3(64), 0, s, a);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const void* V, void* O,
+                              int64_t B, int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim,
+                              const int64_t* q_strides, const int64_t* k_strides,
+                              const int64_t* v_strides, const int64_t* o_strides, float scale,
+                              int causal, const uint8_t* key_valid, int64_t key_valid_sb,
+                              void* stream) {
+  if (B < 0 || H < 0 || S_q < 0 || S_k < 0 || head_dim <= 0) return MI355_E_BAD_SIZE;
+  if (B == 0 || H == 0 || S_q == 0) return MI355_OK;
+  if (!Q || !K || !V || !O || !q_strides || !k_strides || !v_strides || !o_strides)
+    return MI355_E_NULL_POINTER;
+  if (dtype != MI355_F32 && dtype != MI355_F16 && dtype != MI355_BF16) return MI355_E_BAD_DTYPE;
+  if (B > 65535 || H > 65535 || S_q > (int64_t)1 << 30 || S_k > (int64_t)1 << 30)
+    return MI355_E_BAD_SIZE;
+  if (head_dim != 64 && head_dim != 128) return MI355_E_HEAD_DIM;
+  if (!(scale > 0.f)) return MI355_E_UNSUPPORTED;
+  // 16-byte row loads (8-byte output stores): strides in elements must keep that alignment.
+  const int64_t va = dtype == MI355_F32 ? 4 : 8;
+  const int64_t* st[3] = {q_strides, k_strides, v_strides};
+  for (int i = 0; i < 3; ++i)
+    for (int j = 0; j < 3; ++j)
+      if (st[i][j] % va) return MI355_E_ALIGNMENT;
+  for (int j = 0; j < 3; ++j)
+    if (o_strides[j] % 4) return MI355_E_ALIGNMENT;
+  if (!aligned16(Q) || !aligned16(K) || !aligned16(V) ||
+      (reinterpret_cast<uintptr_t>(O) & 7u))
+    return MI355_E_ALIGNMENT;
+
+  AttnArgs a{};
+  a.q = Q;
+  a.k = K;
+  a.v = V;
+  a.o = O;
+  a.qs0 = q_strides[0]; a.qs1 = q_strides[1]; a.qs2 = q_strides[2];
+  a.ks0 = k_strides[0]; a.ks1 = k_strides[1]; a.ks2 = k_strides[2];
+  a.vs0 = v_strides[0]; a.vs1 = v_strides[1]; a.vs2 = v_strides[2];
+  a.os0 = o_strides[0]; a.os1 = o_strides[1]; a.os2 = o_strides[2];
+  a.B = B;
+  a.H = H;
+  a.Sq = S_q;
+  a.Sk = S_k;
+  a.c = scale * 1.4426950408889634f;
+  a.thr = 8.0f / a.c;
+  a.kv = key_valid;
+  a.kv_sb = key_valid_sb;
+  const bool kmask = key_valid != nullptr;
+  const bool cz = causal != 0;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (dtype == MI355_F32) {
+    return head_dim == 64 ? launch_f32<64>(a, cz, kmask, s) : launch_f32<128>(a, cz, kmask, s);
+  }
+  if (dtype == MI355_F16) {
+    return head_dim == 64 ? launch_mfma<_Float16, 64, 4>(a, cz, kmask, s)
+                          : launch_mfma<_Float16, 128, 4>(a, cz, kmask, s);
+  }
+  return head_dim == 64 ? launch_mfma<__bf16, 64, 4>(a, cz, kmask, s)
+                        : launch_mfma<__bf16, 128, 4>(a, cz, kmask, s);
+}

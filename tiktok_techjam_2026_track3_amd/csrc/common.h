@@ -1,0 +1,116 @@
+// Shared device-side types and helpers for the gfx950 kernels of libmi355attn.so.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/mi355attn.h"
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef int32_t i32x16 __attribute__((ext_vector_type(16)));
+typedef int32_t i32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+#define MI355_DEVINL __device__ __forceinline__
+
+// Per-element-type traits for the 32x32 MFMA family used by every kernel here.
+//   vec8  : one 16-byte MFMA operand fragment (8 x 16-bit, 16 x int8 packed in u32x4, 4 x fp32)
+//   acc   : the 32x32 accumulator fragment (16 values per lane)
+//   MFMAS_PER_CHUNK: how many MFMA issues consume one 16-byte fragment per lane
+template <typename T>
+struct Mfma;
+
+template <>
+struct Mfma<_Float16> {
+  using elem = _Float16;
+  using frag = f16x8;
+  using acc = f32x16;
+  static constexpr int ELEMS_PER_CHUNK = 8;
+  static constexpr int MFMAS_PER_CHUNK = 1;
+  static MI355_DEVINL acc mma(frag a, frag b, acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<__bf16> {
+  using elem = __bf16;
+  using frag = bf16x8;
+  using acc = f32x16;
+  static constexpr int ELEMS_PER_CHUNK = 8;
+  static constexpr int MFMAS_PER_CHUNK = 1;
+  static MI355_DEVINL acc mma(frag a, frag b, acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<int8_t> {
+  using elem = int8_t;
+  using frag = i32x4;  // 16 x int8
+  using acc = i32x16;
+  static constexpr int ELEMS_PER_CHUNK = 16;
+  static constexpr int MFMAS_PER_CHUNK = 1;
+  static MI355_DEVINL acc mma(frag a, frag b, acc c) {
+    return __builtin_amdgcn_mfma_i32_32x32x32_i8(a, b, c, 0, 0, 0);
+  }
+};
+
+template <>
+struct Mfma<float> {
+  using elem = float;
+  using frag = f32x4;  // 4 x fp32, consumed one element per MFMA (32x32x2)
+  using acc = f32x16;
+  static constexpr int ELEMS_PER_CHUNK = 4;
+  static constexpr int MFMAS_PER_CHUNK = 4;
+  static MI355_DEVINL acc mma_elem(float a, float b, acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x2f32(a, b, c, 0, 0, 0);
+  }
+  static MI355_DEVINL acc mma(frag a, frag b, acc c) {
+    c = mma_elem(a[0], b[0], c);
+    c = mma_elem(a[1], b[1], c);
+    c = mma_elem(a[2], b[2], c);
+    c = mma_elem(a[3], b[3], c);
+    return c;
+  }
+};
+
+// Accumulator layout of the 32x32 MFMAs (D = A·B, A rows = m, B columns = n):
+// lane l, register i holds D[m][n] with n = l % 32 and m = 8*(i/4) + 4*(l/32) + (i%4).
+// Operand layout: lane l supplies A[m = l%32][k-slice (l/32)] and B[k-slice (l/32)][n = l%32];
+// A and B always use the same k-slice mapping, so any permutation of k inside a slice is sound.
+MI355_DEVINL int mfma_row(int i, int lane) { return ((i >> 2) << 3) + ((lane >> 5) << 2) + (i & 3); }
+
+template <typename T>
+MI355_DEVINL float to_f32(T v) {
+  return static_cast<float>(v);
+}
+
+template <typename T>
+MI355_DEVINL T from_f32(float v) {
+  return static_cast<T>(v);  // round-to-nearest-even for _Float16 / __bf16
+}
+
+// Reductions over the lane pair (l, l ^ 32) with v_permlane32_swap (gfx950). Swapping a value
+// with itself leaves, in every lane, {own, partner} in the two results (which one lands where
+// depends on the lane half), so max/sum of the two is the pair reduction in all 64 lanes.
+MI355_DEVINL float pair_max(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+MI355_DEVINL float pair_sum(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+MI355_DEVINL int elem_size(int dtype) { return dtype == MI355_F32 ? 4 : 2; }
+
+inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

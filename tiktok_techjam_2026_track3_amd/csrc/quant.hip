@@ -1,0 +1,114 @@
+// Per-row symmetric int8 quantisation (activations per token, weights per output channel).
+// One wave per row: pass 1 reduces |x| with 16-byte loads, pass 2 re-reads the row (L1/L2 hit)
+// and writes q = round_half_even(x / s) 16 values per lane-store. Division is IEEE fp32
+// (hipcc's default correctly rounded divide), rounding is v_rndne_f32, so the output is
+// bit-identical to the torch recipe it restates.
+#include "common.h"
+
+namespace {
+
+template <typename T>
+MI355_DEVINL void unpack16(const u32x4& v, float* out8);
+
+template <>
+MI355_DEVINL void unpack16<_Float16>(const u32x4& v, float* o) {
+  const f16x8 h = __builtin_bit_cast(f16x8, v);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = static_cast<float>(h[e]);
+}
+template <>
+MI355_DEVINL void unpack16<__bf16>(const u32x4& v, float* o) {
+  const bf16x8 h = __builtin_bit_cast(bf16x8, v);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = static_cast<float>(h[e]);
+}
+template <>
+MI355_DEVINL void unpack16<float>(const u32x4& v, float* o) {
+#pragma unroll
+  for (int e = 0; e < 4; ++e) o[e] = __uint_as_float(v[e]);
+}
+
+MI355_DEVINL float wave_max(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  return v;
+}
+
+MI355_DEVINL uint32_t pack4_i8(const float* x, float s) {
+  uint32_t w = 0;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    float r = __builtin_rintf(x[e] / s);
+    r = fminf(fmaxf(r, -128.f), 127.f);
+    w |= (static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu) << (8 * e);
+  }
+  return w;
+}
+
+template <typename T>
+__global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ X, int64_t ldx,
+                                                         int8_t* __restrict__ Xq,
+                                                         float* __restrict__ scale, int64_t M,
+                                                         int64_t K, int mode) {
+  constexpr int EPC = 16 / sizeof(T);  // elements per 16-byte load
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const T* xr = X + row * ldx;
+  float amax = 0.f;
+  for (int64_t k = static_cast<int64_t>(lane) * EPC; k < K; k += 64 * EPC) {
+    float f[8];
+    unpack16<T>(*reinterpret_cast<const u32x4*>(xr + k), f);
+#pragma unroll
+    for (int e = 0; e < EPC; ++e) amax = fmaxf(amax, fabsf(f[e]));
+  }
+  amax = wave_max(amax);
+  // mode 0: clamp(amax, 1e-6) / 127 ; mode 1: clamp(amax / 127, 1e-8)
+  const float s = mode == 0 ? fmaxf(amax, 1e-6f) / 127.0f : fmaxf(amax / 127.0f, 1e-8f);
+  if (lane == 0) scale[row] = s;
+  int8_t* qr = Xq + row * K;
+  // 16 outputs per lane per step (one 16-byte store)
+  for (int64_t k = static_cast<int64_t>(lane) * 16; k < K; k += 64 * 16) {
+    float f[16];
+#pragma unroll
+    for (int c = 0; c < 16 / EPC; ++c)
+      unpack16<T>(*reinterpret_cast<const u32x4*>(xr + k + c * EPC), f + c * EPC);
+    u32x4 w;
+#pragma unroll
+    for (int d = 0; d < 4; ++d) w[d] = pack4_i8(f + 4 * d, s);
+    *reinterpret_cast<u32x4*>(qr + k) = w;
+  }
+}
+
+}  // namespace
+
+extern "C" int mi355_quant_rows_i8(int in_dtype, const void* X, int64_t ldx, int8_t* Xq,
+                                   float* scale, int64_t M, int64_t K, int mode, void* stream) {
+  if (M < 0 || K <= 0) return MI355_E_BAD_SIZE;
+  if (M == 0) return MI355_OK;
+  if (!X || !Xq || !scale) return MI355_E_NULL_POINTER;
+  if (mode != 0 && mode != 1) return MI355_E_UNSUPPORTED;
+  if (in_dtype != MI355_F32 && in_dtype != MI355_F16 && in_dtype != MI355_BF16)
+    return MI355_E_BAD_DTYPE;
+  const int64_t epc = in_dtype == MI355_F32 ? 4 : 8;
+  if (K % 16 || ldx % epc || !aligned16(X) || !aligned16(Xq)) return MI355_E_ALIGNMENT;
+  if (ldx < K) return MI355_E_BAD_SIZE;
+  if ((M + 3) / 4 > 0x7fffffffLL) return MI355_E_BAD_SIZE;
+  const dim3 grid(static_cast<unsigned>((M + 3) / 4)), block(256);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (in_dtype) {
+    case MI355_F16:
+      hipLaunchKernelGGL(quant_rows_kernel<_Float16>, grid, block, 0, s,
+                         static_cast<const _Float16*>(X), ldx, Xq, scale, M, K, mode);
+      break;
+    case MI355_BF16:
+      hipLaunchKernelGGL(quant_rows_kernel<__bf16>, grid, block, 0, s,
+                         static_cast<const __bf16*>(X), ldx, Xq, scale, M, K, mode);
+      break;
+    default:
+      hipLaunchKernelGGL(quant_rows_kernel<float>, grid, block, 0, s,
+                         static_cast<const float*>(X), ldx, Xq, scale, M, K, mode);
+      break;
+  }
+  return static_cast<int>(hipGetLastError());
+}

@@ -1,0 +1,180 @@
+"""Torch-facing wrappers of the libmi355attn entry points.
+
+Each wrapper validates shapes/dtypes/devices on the host, allocates outputs with torch (the
+library never allocates), and enqueues the kernel on torch's current stream of the tensors'
+device. Nothing here synchronises the host, so the calls are hipGraph-capturable.
+"""
+from __future__ import annotations
+
+from typing import Optional, Tuple
+
+import torch
+
+from . import _lib
+
+
+def _stream(t: torch.Tensor) -> int:
+    return torch.cuda.current_stream(t.device).cuda_stream
+
+
+def _on_gpu(*tensors: Optional[torch.Tensor]) -> torch.device:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if t.device.type != "cuda":
+            raise ValueError(f"expected a GPU tensor, got one on {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+    if dev is None:
+        raise ValueError("no tensor given")
+    return dev
+
+
+def _mask_ptr(mask: Optional[torch.Tensor], shape: Tuple[int, ...]) -> int:
+    if mask is None:
+        return 0
+    if mask.dtype not in (torch.bool, torch.uint8):
+        raise TypeError("masks must be bool or uint8")
+    if tuple(mask.shape) != tuple(shape) or not mask.is_contiguous():
+        raise ValueError(f"mask must be a contiguous tensor of shape {shape}")
+    return mask.data_ptr()
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
+           out: Optional[torch.Tensor] = None, row_valid: Optional[torch.Tensor] = None,
+           out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``out[M, N] = x[M, K] @ weight[N, K]^T + bias[N]`` (nn.Linear), fp32 accumulate.
+
+    ``x`` may be a row-strided 2-D view (unit column stride); ``weight`` must be contiguous and
+    of x's dtype; ``bias`` is fp32. ``out_dtype`` (default x's dtype) may be the other 16-bit
+    type for 16-bit inputs. Rows whose ``row_valid`` entry is False are written as zeros.
+    """
+    _on_gpu(x, weight, bias, out, row_valid)
+    if x.dim() != 2 or weight.dim() != 2:
+        raise ValueError("linear expects 2-D x and weight")
+    M, K = x.shape
+    N, K2 = weight.shape
+    if K2 != K:
+        raise ValueError(f"inner sizes differ: x has K={K}, weight has K={K2}")
+    dt = x.dtype
+    odt = out_dtype or (out.dtype if out is not None else dt)
+    if weight.dtype != dt:
+        raise TypeError("x and weight must share one dtype")
+    if x.stride(1) != 1 or not weight.is_contiguous():
+        raise ValueError("x needs unit column stride and weight must be contiguous")
+    if bias is not None and (bias.shape != (N,) or bias.dtype != torch.float32
+                             or not bias.is_contiguous()):
+        raise ValueError(f"bias must be a contiguous fp32 tensor of shape ({N},)")
+    if out is None:
+        out = torch.empty((M, N), device=x.device, dtype=odt)
+    elif out.shape != (M, N) or out.dtype != odt or out.stride(1) != 1:
+        raise ValueError("out must be [M, N] of out_dtype with unit column stride")
+    st = _lib.lib().mi355_gemm_bias(
+        _lib.dtype_code(dt), _lib.dtype_code(odt), x.data_ptr(), x.stride(0), weight.data_ptr(),
+        weight.stride(0), bias.data_ptr() if bias is not None else 0, out.data_ptr(),
+        out.stride(0), M, N, K, _mask_ptr(row_valid, (M,)), _stream(x))
+    _lib.check("mi355_gemm_bias", st)
+    return out
+
+
+def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[torch.Tensor] = None,
+              scale: Optional[float] = None, causal: bool = False,
+              key_valid: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """Streamed softmax attention over ``[B, S, H, head_dim]`` views (unit head_dim stride).
+
+    ``out`` defaults to a new contiguous ``[B, S_q, H, head_dim]`` tensor, whose
+    ``view(B, S_q, H * head_dim)`` is the merged-head context of the reference block.
+    ``key_valid`` is an optional ``[B, S_k]`` bool mask of keys to attend to.
+    """
+    _on_gpu(q, k, v, out, key_valid)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be 4-D [B, S, H, head_dim] views")
+    B, Sq, H, D = q.shape
+    Bk, Sk, Hk, Dk = k.shape
+    if (Bk, Hk, Dk) != (B, H, D) or tuple(v.shape) != (B, Sk, H, D):
+        raise ValueError(f"shape mismatch q={tuple(q.shape)} k={tuple(k.shape)} v={tuple(v.shape)}")
+    dt = q.dtype
+    if k.dtype != dt or v.dtype != dt:
+        raise TypeError("q, k, v must share one dtype")
+    if q.stride(3) != 1 or k.stride(3) != 1 or v.stride(3) != 1:
+        raise ValueError("head_dim must be the unit-stride dimension")
+    if out is None:
+        out = torch.empty((B, Sq, H, D), device=q.device, dtype=dt)
+    elif tuple(out.shape) != (B, Sq, H, D) or out.dtype != dt or out.stride(3) != 1:
+        raise ValueError("out must be [B, S_q, H, head_dim] of q's dtype with unit head_dim stride")
+    if scale is None:
+        scale = D ** -0.5
+    kv_ptr, kv_sb = 0, 0
+    if key_valid is not None:
+        kv_ptr = _mask_ptr(key_valid, (B, Sk))
+        kv_sb = key_valid.stride(0)
+    L = _lib
+    st = L.lib().mi355_attn_fwd(
+        L.dtype_code(dt), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq, Sk, D,
+        L.i64_array((q.stride(0), q.stride(1), q.stride(2))),
+        L.i64_array((k.stride(0), k.stride(1), k.stride(2))),
+        L.i64_array((v.stride(0), v.stride(1), v.stride(2))),
+        L.i64_array((out.stride(0), out.stride(1), out.stride(2))),
+        float(scale), 1 if causal else 0, kv_ptr, kv_sb, _stream(q))
+    L.check("mi355_attn_fwd", st)
+    return out
+
+
+def quant_rows_i8(x: torch.Tensor, mode: int = 0) -> Tuple[torch.Tensor, torch.Tensor]:
+    """Per-row symmetric int8 quantisation; returns ``(q [M, K] int8, scale [M] fp32)``.
+
+    mode 0 is the activation recipe (scale = max(amax, 1e-6) / 127), mode 1 the weight recipe
+    (scale = max(amax / 127, 1e-8)).
+    """
+    _on_gpu(x)
+    if x.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("quant_rows_i8 expects a 2-D tensor with unit column stride")
+    M, K = x.shape
+    q = torch.empty((M, K), device=x.device, dtype=torch.int8)
+    s = torch.empty((M,), device=x.device, dtype=torch.float32)
+    st = _lib.lib().mi355_quant_rows_i8(_lib.dtype_code(x.dtype), x.data_ptr(), x.stride(0),
+                                        q.data_ptr(), s.data_ptr(), M, K, int(mode), _stream(x))
+    _lib.check("mi355_quant_rows_i8", st)
+    return q, s
+
+
+def linear_i8(a: torch.Tensor, w: torch.Tensor, s_a: torch.Tensor, s_w: torch.Tensor,
+              bias: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.float16,
+              out: Optional[torch.Tensor] = None, acc_out: Optional[torch.Tensor] = None,
+              row_valid: Optional[torch.Tensor] = None, want_out: bool = True) -> Optional[torch.Tensor]:
+    """W8A8 projection: ``out = fp32(a @ w^T) * (s_a[:, None] * s_w[None, :]) + bias``.
+
+    ``a`` is ``[M, K]`` int8, ``w`` is ``[N, K]`` int8 (K-major), scales fp32. ``acc_out``
+    (``[M, N]`` int32) receives the raw int32 accumulators when given.
+    """
+    _on_gpu(a, w, s_a, s_w, bias, out, acc_out, row_valid)
+    if a.dtype != torch.int8 or w.dtype != torch.int8:
+        raise TypeError("a and w must be int8")
+    if not a.is_contiguous() or not w.is_contiguous():
+        raise ValueError("a and w must be contiguous")
+    M, K = a.shape
+    N, K2 = w.shape
+    if K2 != K:
+        raise ValueError("inner sizes differ")
+    if s_a.shape != (M,) or s_w.shape != (N,) or s_a.dtype != torch.float32 or s_w.dtype != torch.float32:
+        raise ValueError("s_a [M] and s_w [N] must be fp32")
+    if bias is not None and (bias.shape != (N,) or bias.dtype != torch.float32):
+        raise ValueError("bias must be fp32 [N]")
+    if acc_out is not None and (acc_out.shape != (M, N) or acc_out.dtype != torch.int32
+                                or not acc_out.is_contiguous()):
+        raise ValueError("acc_out must be a contiguous int32 [M, N] tensor")
+    if want_out and out is None:
+        out = torch.empty((M, N), device=a.device, dtype=out_dtype)
+    if out is not None and (out.shape != (M, N) or out.dtype != out_dtype or out.stride(1) != 1):
+        raise ValueError("out must be [M, N] of out_dtype with unit column stride")
+    st = _lib.lib().mi355_gemm_i8(
+        a.data_ptr(), w.data_ptr(), s_a.data_ptr(), s_w.data_ptr(),
+        bias.data_ptr() if bias is not None else 0, _lib.dtype_code(out_dtype),
+        out.data_ptr() if out is not None else 0, out.stride(0) if out is not None else N,
+        acc_out.data_ptr() if acc_out is not None else 0, M, N, K,
+        _mask_ptr(row_valid, (M,)), _stream(a))
+    _lib.check("mi355_gemm_i8", st)
+    return out
