@@ -37,7 +37,7 @@ import torch.nn as nn
 
 from . import ops
 
-_CACHE_KEYS = ("_mi355_pack", "_mi355_mask")
+_CACHE_KEYS = ("_mi355_pack",)
 
 
 class SelfAttention(nn.Module):
@@ -111,9 +111,10 @@ class SelfAttention(nn.Module):
     def _resolve_mask(self, mask: Optional[torch.Tensor], B: int, S: int, device: torch.device):
         """Returns (key_valid [B,S] bool or None, row_valid [B*S] bool or None).
 
-        An all-true mask is dropped (its masked_fill calls are identities); deciding that needs
-        one host sync per distinct mask tensor, cached by identity and version as the
-        reference's dispatcher does (dispatcher_region.py:1102-1146).
+        A given mask always goes to the kernels: the attention kernel ballots the mask bytes of
+        each key tile and masks element-wise only where a tile holds invalid keys, so an
+        all-true mask costs one byte load per key per work-group and no host synchronisation
+        (unlike an "is it all true?" check on the host).
         """
         if mask is None:
             return None, None
@@ -121,16 +122,7 @@ class SelfAttention(nn.Module):
             raise ValueError(f"valid_token_mask must be a bool tensor of shape ({B}, {S})")
         if mask.device != device:
             raise ValueError("valid_token_mask must be on the input's device")
-        stamp = (id(mask), mask.data_ptr(), mask._version)
-        cached = self.__dict__.get("_mi355_mask")
-        if cached is not None and cached[0] == stamp:
-            all_true = cached[1]
-        else:
-            all_true = bool(mask.all().item())
-            self.__dict__["_mi355_mask"] = (stamp, all_true)
-        if all_true:
-            return None, None
-        m = mask.contiguous()
+        m = mask if mask.is_contiguous() else mask.contiguous()
         return m, m.view(B * S)
 
     # ----------------------------------------------------------------------------- forward

@@ -105,8 +105,11 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
   const int n_kt = static_cast<int>((kend + BN - 1) / BN);
 
   u32x4 rk[K_LOADS], rv0[V_UNITS], rv1[V_UNITS];
+  // key-validity byte of key (tile start + lane), fetched one tile ahead with K/V
+  uint32_t kv_next = 1u, kv_cur = 1u;
   auto load_global = [&](int j) {
     const int64_t k0 = static_cast<int64_t>(j) * BN;
+    if constexpr (KMASK) kv_next = (k0 + lane < p.Sk) ? kvb[k0 + lane] : 0u;
 #pragma unroll
     for (int i = 0; i < K_LOADS; ++i) {
       const int idx = tid + i * NT, key = idx / KCH, ch = idx % KCH;
@@ -163,6 +166,7 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
 
   for (int j = 0; j < n_kt; ++j) {
     const int cur = j & 1;
+    if constexpr (KMASK) kv_cur = kv_next;
     if (j + 1 < n_kt) load_global(j + 1);
 
     // S^T tile: 64 keys x 32 queries per wave.
@@ -181,16 +185,19 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
     }
 
     const int64_t k0 = static_cast<int64_t>(j) * BN;
-    const bool need_mask = KMASK || (k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > q_wg);
+    // tile validity word: bit kk set <=> key k0 + kk is in range (and valid under the mask)
+    uint64_t vbits = ~0ull;
+    if constexpr (KMASK) vbits = __builtin_amdgcn_ballot_w64(kv_cur != 0u);
+    const bool need_mask = (vbits != ~0ull) || (k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > q_wg);
     if (need_mask) {
 #pragma unroll
       for (int t = 0; t < 2; ++t)
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
-          const int64_t key = k0 + 32 * t + mfma_row(i, lane);
-          bool ok = key < p.Sk;
+          const int kk = 32 * t + mfma_row(i, lane);
+          const int64_t key = k0 + kk;
+          bool ok = key < p.Sk && ((vbits >> kk) & 1ull);
           if (CAUSAL) ok = ok && key <= qi;
-          if (KMASK) ok = ok && kvb[key < p.Sk ? key : 0] != 0;
           if (!ok) sacc[t][i] = NEG_INF;
         }
     }
