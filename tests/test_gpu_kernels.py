@@ -3,10 +3,11 @@
 Floating-point kernels are checked against an fp64 evaluation of the same (already rounded)
 inputs with an explicit error bound built from the rounding points of the kernel:
   GEMM:      |out - ref| <= u_out*|ref| + 4*K*2^-24 * (|A|·|W|^T) + 1e-7
-  attention: |out - ref| <= (2*u_p + 2^-18 + 2^-22*L) * (P·|V|) + u_out*|ref| + 1e-7
+  attention: |out - ref| <= (2*u_p + 2^-18 + 2^-22*L + 2 ln2 u_in c max_j |q_i|.|k_j|) * (P·|V|)
+                             + u_out*|ref| + 1e-7
 where u = 2^-11 (fp16), 2^-8 (bf16), 2^-24 (fp32) is the unit round-off of the type the value is
-rounded to (probabilities P for u_p, the stored output for u_out) and L = max|s*scale*log2(e)|
-(the exp2 argument's fp32 rounding). The int8 kernels are compared bit for bit.
+rounded to (probabilities P for u_p, the stored output for u_out), L = max|s*scale*log2(e)|
+(the exp2 argument's fp32 rounding) and c = scale*log2(e) (the kernel re-rounds c*q). The int8 kernels are compared bit for bit.
 """
 import math
 
@@ -114,10 +115,15 @@ def _attn_check(gpu, dtype, B, H, Sq, Sk, hd, causal, key_valid=None, packed=Fal
     ref = OA.attention_core(tq, tk, tv, hd ** -0.5, causal, key_valid).transpose(1, 2)
     pav = OA.attention_core(tq, tk, tv.abs(), hd ** -0.5, causal, key_valid).transpose(1, 2)
     up = UNIT[dtype] if dtype != torch.float32 else 2.0 ** -22
-    # the exp2 argument s*scale*log2e - m carries an fp32 rounding error relative to its
-    # largest magnitude: allow 2^-22 * max|logit2| relative error on every probability
-    logit2 = (tq @ tk.transpose(-2, -1)).abs().max().item() * hd ** -0.5 * 1.4426950408889634
-    bound = (2 * up + 2.0 ** -18 + 2.0 ** -22 * logit2) * pav + UNIT[dtype] * ref.abs() + 1e-7
+    c = hd ** -0.5 * 1.4426950408889634
+    # the exp2 argument s*c - m carries an fp32 rounding error relative to its largest
+    # magnitude: allow 2^-22 * max|logit2| relative error on every probability
+    logit2 = (tq @ tk.transpose(-2, -1)).abs().max().item() * c
+    # the kernel rounds c*q back to the input dtype: |d s*c| <= u_in * c * (|q|.|k|) per score
+    qk_abs = (tq.abs() @ tk.abs().transpose(-2, -1)).amax(dim=-1, keepdim=True).transpose(1, 2)
+    uq = UNIT[dtype] if dtype != torch.float32 else 0.0
+    rel = 2 * up + 2.0 ** -18 + 2.0 ** -22 * logit2 + 2 * math.log(2) * uq * c * qk_abs
+    bound = rel * pav + UNIT[dtype] * ref.abs() + 1e-7
     finite = torch.isfinite(ref)
     assert torch.equal(torch.isfinite(out), finite)
     err = (out - ref).abs()[finite]

@@ -10,8 +10,10 @@
 //     (the rounding point of torch_transformer_benchmark.py:111) and fed straight from registers
 //     as the B operand of O^T += V^T · P^T; V^T comes from an LDS tile that the loader writes
 //     transposed, with keys permuted inside 16-key groups so every A fragment is one 16-byte read;
-//   * the running max is only moved when a tile's max exceeds it by more than 8 (log2 units), so
-//     the O/l rescale is skipped on most tiles; unnormalised probabilities stay <= 2^8;
+//   * scores live in the log2 domain (Q pre-multiplied by scale*log2e) and every score MFMA chain
+//     starts from -mu, so exp2 consumes the MFMA output directly;
+//   * the running max mu is only moved when a tile's max exceeds it by more than 8, so the O/l
+//     rescale is skipped on most tiles; unnormalised probabilities stay <= 2^8;
 //   * causal work-groups stop at the diagonal, mask only tiles that cross it, and are issued
 //     longest-first.
 // fp32 kernel: one query per lane on VALU (the fp32 configuration is launch-latency bound).
@@ -30,7 +32,6 @@ struct AttnArgs {
   int64_t os0, os1, os2;
   int64_t B, H, Sq, Sk;
   float c;    // scale * log2(e)
-  float thr;  // lazy-rescale threshold in raw score units (8 / c)
   const uint8_t* kv;
   int64_t kv_sb;
   int n_qtiles;
@@ -62,20 +63,51 @@ MI355_DEVINL typename Mfma<T>::frag pack8(const float* p) {
   return f;
 }
 
-template <typename T, int HD, int NW, bool CAUSAL, bool KMASK>
+// Sum of the 8 probabilities of one fragment into an fp32 accumulator (v_dot2 with ones): the
+// row sum is taken over the same rounded values that feed P·V.
+MI355_DEVINL float frag_sum(f16x8 f, float acc) {
+  const f16x2 one = {(_Float16)1.0f, (_Float16)1.0f};
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const f16x2 pr = {f[2 * r], f[2 * r + 1]};
+    acc = __builtin_amdgcn_fdot2(pr, one, acc, false);
+  }
+  return acc;
+}
+MI355_DEVINL float frag_sum(bf16x8 f, float acc) {
+  const bf16x2 one = {(__bf16)1.0f, (__bf16)1.0f};
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const bf16x2 pr = {f[2 * r], f[2 * r + 1]};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(pr, one, acc, false);
+  }
+  return acc;
+}
+
+// QG query groups of 32 per wave: every K / V^T fragment read from LDS feeds QG MFMAs.
+//
+// Scores are kept in the log2 domain: the Q fragments are multiplied once by c = scale*log2(e)
+// (re-rounded to the input dtype), and each score MFMA chain starts from a block holding -mu, the
+// running (lazy) max, so the MFMA output is already s*c - mu and feeds v_exp_f32 directly.
+template <typename T, int HD, int NW, int QG, bool CAUSAL, bool KMASK>
 __global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
-  constexpr int BM = NW * 32;
-  constexpr int BN = 64;
+  constexpr int QW = 32 * QG;   // queries per wave
+  constexpr int BM = NW * QW;   // queries per work-group
+  constexpr int BN = 64;        // keys per tile
   constexpr int NT = NW * 64;
   constexpr int KCH = HD / 8;   // 16-byte chunks per K row
   constexpr int VCH = BN / 8;   // 16-byte chunks per V^T row
   constexpr int KS = HD / 16;   // MFMA k-steps of S^T
   constexpr int MT = HD / 32;   // 32-row tiles of O^T
-  constexpr int K_LOADS = BN * KCH / NT;
-  constexpr int V_UNITS = (BN / 2) * KCH / NT;
-  static_assert(K_LOADS >= 1 && V_UNITS >= 1, "tile/thread shape");
+  // loader work: K as 16-byte chunks, V as (key pair, 16-byte chunk) units; threads beyond the
+  // unit count idle in the loader when the work-group is larger than the tile
+  constexpr int K_UNITS_ALL = BN * KCH, V_UNITS_ALL = (BN / 2) * KCH;
+  constexpr int K_LOADS = (K_UNITS_ALL + NT - 1) / NT;
+  constexpr int V_UNITS = (V_UNITS_ALL + NT - 1) / NT;
+  static_assert(K_UNITS_ALL % NT == 0 || NT % K_UNITS_ALL == 0, "K loader shape");
+  static_assert(V_UNITS_ALL % NT == 0 || NT % V_UNITS_ALL == 0, "V loader shape");
 
   __shared__ u32x4 k_lds[2][BN * KCH];
   __shared__ u32x4 vt_lds[2][HD * VCH];
@@ -85,20 +117,32 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
   const int qt = CAUSAL ? (p.n_qtiles - 1 - static_cast<int>(blockIdx.x)) : static_cast<int>(blockIdx.x);
   const int64_t h = blockIdx.y, b = blockIdx.z;
   const int64_t q_wg = static_cast<int64_t>(qt) * BM;
-  const int64_t qi = q_wg + wave * 32 + l32;
+  const int64_t q_wave = q_wg + wave * QW;  // first query of this wave
 
   const T* __restrict__ Qb = static_cast<const T*>(p.q) + b * p.qs0 + h * p.qs2;
-  const T* __restrict__ Kb = static_cast<const T*>(p.k) + b * p.ks0 + h * p.ks2;
-  const T* __restrict__ Vb = static_cast<const T*>(p.v) + b * p.vs0 + h * p.vs2;
+  const char* __restrict__ Kb = reinterpret_cast<const char*>(static_cast<const T*>(p.k) + b * p.ks0 + h * p.ks2);
+  const char* __restrict__ Vb = reinterpret_cast<const char*>(static_cast<const T*>(p.v) + b * p.vs0 + h * p.vs2);
   const uint8_t* __restrict__ kvb = KMASK ? p.kv + b * p.kv_sb : nullptr;
+  const int Sk = static_cast<int>(p.Sk);
+  // row strides in bytes; the entry point guarantees 64 rows of them fit in 32 bits
+  const uint32_t kstride = static_cast<uint32_t>(p.ks1) * sizeof(T);
+  const uint32_t vstride = static_cast<uint32_t>(p.vs1) * sizeof(T);
 
-  // Q^T fragments: lane (query qi, slice g) holds Q[qi][16*ks + 8*g .. +7].
-  frag qf[KS];
+  // Q^T fragments pre-scaled by c: group n, lane (query q_wave + 32n + l32, slice g) holds
+  // c * Q[q][16*s + 8*g .. +7].
+  frag qf[QG][KS];
 #pragma unroll
-  for (int s = 0; s < KS; ++s) {
-    u32x4 v = {0u, 0u, 0u, 0u};
-    if (qi < p.Sq) v = *reinterpret_cast<const u32x4*>(Qb + qi * p.qs1 + 16 * s + 8 * g);
-    qf[s] = __builtin_bit_cast(frag, v);
+  for (int n = 0; n < QG; ++n) {
+    const int64_t qi = q_wave + 32 * n + l32;
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u32x4 v = {0u, 0u, 0u, 0u};
+      if (qi < p.Sq) v = *reinterpret_cast<const u32x4*>(Qb + qi * p.qs1 + 16 * s + 8 * g);
+      frag f = __builtin_bit_cast(frag, v);
+#pragma unroll
+      for (int r = 0; r < 8; ++r) f[r] = from_f32<T>(to_f32(f[r]) * p.c);
+      qf[n][s] = f;
+    }
   }
 
   const int64_t kend = CAUSAL ? ((q_wg + BM) < p.Sk ? (q_wg + BM) : p.Sk) : p.Sk;
@@ -108,23 +152,27 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
   // key-validity byte of key (tile start + lane), fetched one tile ahead with K/V
   uint32_t kv_next = 1u, kv_cur = 1u;
   auto load_global = [&](int j) {
-    const int64_t k0 = static_cast<int64_t>(j) * BN;
-    if constexpr (KMASK) kv_next = (k0 + lane < p.Sk) ? kvb[k0 + lane] : 0u;
+    const int k0 = j * BN;
+    // tile base in scalar registers, per-lane offsets in 32 bits
+    const char* kt = Kb + static_cast<int64_t>(k0) * kstride;
+    const char* vt = Vb + static_cast<int64_t>(k0) * vstride;
+    if constexpr (KMASK) kv_next = (k0 + lane < Sk) ? kvb[k0 + lane] : 0u;
 #pragma unroll
     for (int i = 0; i < K_LOADS; ++i) {
       const int idx = tid + i * NT, key = idx / KCH, ch = idx % KCH;
-      const int64_t gk = k0 + key;
       u32x4 v = {0u, 0u, 0u, 0u};
-      if (gk < p.Sk) v = *reinterpret_cast<const u32x4*>(Kb + gk * p.ks1 + ch * 8);
+      if (idx < K_UNITS_ALL && k0 + key < Sk)
+        v = *reinterpret_cast<const u32x4*>(kt + (static_cast<uint32_t>(key) * kstride + ch * 16u));
       rk[i] = v;
     }
 #pragma unroll
     for (int i = 0; i < V_UNITS; ++i) {
       const int u = tid + i * NT, pr = u % 32, ch = u / 32;
-      const int64_t gk = k0 + 2 * pr;
+      const uint32_t off = static_cast<uint32_t>(2 * pr) * vstride + ch * 16u;
       u32x4 a = {0u, 0u, 0u, 0u}, c = {0u, 0u, 0u, 0u};
-      if (gk < p.Sk) a = *reinterpret_cast<const u32x4*>(Vb + gk * p.vs1 + ch * 8);
-      if (gk + 1 < p.Sk) c = *reinterpret_cast<const u32x4*>(Vb + (gk + 1) * p.vs1 + ch * 8);
+      if (u < V_UNITS_ALL && k0 + 2 * pr < Sk) a = *reinterpret_cast<const u32x4*>(vt + off);
+      if (u < V_UNITS_ALL && k0 + 2 * pr + 1 < Sk)
+        c = *reinterpret_cast<const u32x4*>(vt + (off + vstride));
       rv0[i] = a;
       rv1[i] = c;
     }
@@ -133,12 +181,13 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
 #pragma unroll
     for (int i = 0; i < K_LOADS; ++i) {
       const int idx = tid + i * NT, key = idx / KCH, ch = idx % KCH;
-      k_lds[s][key * KCH + (ch ^ swz<KCH>(key))] = rk[i];
+      if (idx < K_UNITS_ALL) k_lds[s][key * KCH + (ch ^ swz<KCH>(key))] = rk[i];
     }
     uint32_t* vt32 = reinterpret_cast<uint32_t*>(&vt_lds[s][0]);
 #pragma unroll
     for (int i = 0; i < V_UNITS; ++i) {
       const int u = tid + i * NT, pr = u % 32, ch = u / 32;
+      if (u >= V_UNITS_ALL) continue;
       const int pos = vt_pos(2 * pr);
       const int pch = pos >> 3, pw = (pos & 7) >> 1;
 #pragma unroll
@@ -151,12 +200,21 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
     }
   };
 
-  f32x16 oacc[MT];
+  f32x16 oacc[QG][MT];
+  f32x16 negmu[QG];       // -mu replicated: the starting accumulator of every score chain
+  float lsum[QG];
+  bool started[QG];       // a finite tile max has been seen (mu is meaningful)
 #pragma unroll
-  for (int t = 0; t < MT; ++t)
+  for (int n = 0; n < QG; ++n) {
 #pragma unroll
-    for (int i = 0; i < 16; ++i) oacc[t][i] = 0.f;
-  float m_used = NEG_INF, mu = 0.f, lsum = 0.f;
+    for (int t = 0; t < MT; ++t)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) oacc[n][t][i] = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) negmu[n][i] = 0.f;
+    lsum[n] = 0.f;
+    started[n] = false;
+  }
 
   if (n_kt > 0) {
     load_global(0);
@@ -164,109 +222,165 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
   }
   __syncthreads();
 
-  for (int j = 0; j < n_kt; ++j) {
-    const int cur = j & 1;
+  const int q_wave32 = static_cast<int>(q_wave);
+  const float thr = 8.0f;  // log2 units: unnormalised probabilities stay <= 2^8
+
+  auto tile = [&](const int j, const int cur) {
     if constexpr (KMASK) kv_cur = kv_next;
     if (j + 1 < n_kt) load_global(j + 1);
+    const int k0 = j * BN;
 
-    // S^T tile: 64 keys x 32 queries per wave.
-    f32x16 sacc[2];
+    // a wave whose queries all precede this key tile has nothing to add (causal)
+    if (!CAUSAL || k0 <= q_wave32 + QW - 1) {
+      auto kfrag = [&](int t, int s) {
+        const int krow = 32 * t + l32, c = 2 * s + g;
+        return __builtin_bit_cast(frag, k_lds[cur][krow * KCH + (c ^ swz<KCH>(krow))]);
+      };
+      auto vfrag = [&](int mt, int t, int hh) {
+        const int vrow = 32 * mt + l32, c = 4 * t + 2 * hh + g;
+        return __builtin_bit_cast(frag, vt_lds[cur][vrow * VCH + (c ^ swz<VCH>(vrow))]);
+      };
+      // S^T tile (log2 domain, minus mu): 64 keys x QW queries; the K fragments of one 32-key
+      // half are read before its MFMA chain.
+      f32x16 sacc[QG][2];
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
+      for (int t = 0; t < 2; ++t) {
+        frag kf[KS];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) sacc[t][i] = 0.f;
-      const int krow = 32 * t + l32;
+        for (int s = 0; s < KS; ++s) kf[s] = kfrag(t, s);
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        const int c = 2 * s + g;
-        const u32x4 a = k_lds[cur][krow * KCH + (c ^ swz<KCH>(krow))];
-        sacc[t] = MF::mma(__builtin_bit_cast(frag, a), qf[s], sacc[t]);
-      }
-    }
-
-    const int64_t k0 = static_cast<int64_t>(j) * BN;
-    // tile validity word: bit kk set <=> key k0 + kk is in range (and valid under the mask)
-    uint64_t vbits = ~0ull;
-    if constexpr (KMASK) vbits = __builtin_amdgcn_ballot_w64(kv_cur != 0u);
-    const bool need_mask = (vbits != ~0ull) || (k0 + BN > p.Sk) || (CAUSAL && k0 + BN - 1 > q_wg);
-    if (need_mask) {
+        for (int n = 0; n < QG; ++n) {
+          sacc[n][t] = MF::mma(kf[0], qf[n][0], negmu[n]);
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kk = 32 * t + mfma_row(i, lane);
-          const int64_t key = k0 + kk;
-          bool ok = key < p.Sk && ((vbits >> kk) & 1ull);
-          if (CAUSAL) ok = ok && key <= qi;
-          if (!ok) sacc[t][i] = NEG_INF;
+          for (int s = 1; s < KS; ++s) sacc[n][t] = MF::mma(kf[s], qf[n][s], sacc[n][t]);
         }
-    }
-
-    float mx = NEG_INF;
-#pragma unroll
-    for (int t = 0; t < 2; ++t)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[t][i]);
-    mx = pair_max(mx);
-
-    if (__builtin_amdgcn_ballot_w64(mx > m_used + p.thr) != 0) {
-      const float m_new = fmaxf(m_used, mx);
-      const float alpha = (m_used == NEG_INF) ? 0.f : fast_exp2((m_used - m_new) * p.c);
-      lsum *= alpha;
-#pragma unroll
-      for (int t = 0; t < MT; ++t)
-#pragma unroll
-        for (int i = 0; i < 16; ++i) oacc[t][i] *= alpha;
-      m_used = m_new;
-      mu = (m_used == NEG_INF) ? 0.f : m_used * p.c;
-    }
-
-    frag pf[2][2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      float pv[16];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        pv[i] = fast_exp2(__builtin_fmaf(sacc[t][i], p.c, -mu));
-        lsum += pv[i];
       }
-      pf[t][0] = pack8<T>(pv);
-      pf[t][1] = pack8<T>(pv + 8);
-    }
+      // with head_dim 64 the whole V^T tile (32 VGPRs per lane) is read ahead of the softmax
+      constexpr bool V_AHEAD = (HD == 64);
+      frag vf[V_AHEAD ? MT : 1][2][2];
+      if constexpr (V_AHEAD) {
+#pragma unroll
+        for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int hh = 0; hh < 2; ++hh) vf[mt][t][hh] = vfrag(mt, t, hh);
+      }
 
-    // O^T (hd x 32 queries) += V^T (hd x 64 keys) . P^T (64 keys x 32 queries)
+      // tile validity word: bit kk set <=> key k0 + kk is valid under the key mask
+      uint64_t vbits = ~0ull;
+      if constexpr (KMASK) vbits = __builtin_amdgcn_ballot_w64(kv_cur != 0u);
+      const bool need_mask =
+          (vbits != ~0ull) || (k0 + BN > Sk) || (CAUSAL && k0 + BN - 1 > q_wave32);
+      if (need_mask) {
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int vrow = 32 * mt + l32;
+        for (int n = 0; n < QG; ++n) {
+          const int qi = q_wave32 + 32 * n + l32;
 #pragma unroll
-      for (int t = 0; t < 2; ++t)
+          for (int t = 0; t < 2; ++t)
 #pragma unroll
-        for (int hh = 0; hh < 2; ++hh) {
-          const int c = 4 * t + 2 * hh + g;
-          const u32x4 a = vt_lds[cur][vrow * VCH + (c ^ swz<VCH>(vrow))];
-          oacc[mt] = MF::mma(__builtin_bit_cast(frag, a), pf[t][hh], oacc[mt]);
+            for (int i = 0; i < 16; ++i) {
+              const int kk = 32 * t + mfma_row(i, lane);
+              const int key = k0 + kk;
+              bool ok = key < Sk && ((vbits >> kk) & 1ull);
+              if (CAUSAL) ok = ok && key <= qi;
+              if (!ok) sacc[n][t][i] = NEG_INF;
+            }
         }
+      }
+
+      frag pf[QG][2][2];
+#pragma unroll
+      for (int n = 0; n < QG; ++n) {
+        float mx = NEG_INF;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[n][t][i]);
+        mx = pair_max(mx);
+        // move mu only when the tile max exceeds it by more than thr (or on the first finite tile)
+        const bool grow = started[n] ? (mx > thr) : (mx != NEG_INF);
+        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+          const float shift = grow ? mx : 0.f;
+          const float alpha = started[n] ? fast_exp2(-shift) : 1.f;
+          lsum[n] *= alpha;
+#pragma unroll
+          for (int t = 0; t < MT; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) oacc[n][t][i] *= alpha;
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sacc[n][t][i] -= shift;
+#pragma unroll
+          for (int i = 0; i < 16; ++i) negmu[n][i] -= shift;
+          started[n] = started[n] || grow;
+        }
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          float pv[16];
+#pragma unroll
+          for (int i = 0; i < 16; ++i) pv[i] = fast_exp2(sacc[n][t][i]);
+          pf[n][t][0] = pack8<T>(pv);
+          pf[n][t][1] = pack8<T>(pv + 8);
+          lsum[n] = frag_sum(pf[n][t][0], lsum[n]);
+          lsum[n] = frag_sum(pf[n][t][1], lsum[n]);
+        }
+      }
+
+      // O^T (hd x QW) += V^T (hd x 64 keys) . P^T (64 keys x QW)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        frag vm[2][2];
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh) {
+            if constexpr (V_AHEAD)
+              vm[t][hh] = vf[mt][t][hh];
+            else
+              vm[t][hh] = vfrag(mt, t, hh);
+          }
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+            for (int n = 0; n < QG; ++n) oacc[n][mt] = MF::mma(vm[t][hh], pf[n][t][hh], oacc[n][mt]);
+      }
     }
 
     if (j + 1 < n_kt) store_lds(cur ^ 1);
     __syncthreads();
-  }
+  };
 
-  const float ltot = pair_sum(lsum);
-  const float inv = 1.0f / ltot;
-  if (qi < p.Sq) {
-    T* Ob = static_cast<T*>(p.o) + b * p.os0 + qi * p.os1 + h * p.os2;
+  // two tiles per trip: the LDS stage of each is a compile-time constant
+  int j = 0;
+  for (; j + 1 < n_kt; j += 2) {
+    tile(j, 0);
+    tile(j + 1, 1);
+  }
+  if (j < n_kt) tile(j, 0);
+
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
+  for (int n = 0; n < QG; ++n) {
+    const int64_t qi = q_wave + 32 * n + l32;
+    const float ltot = pair_sum(lsum[n]);
+    const float inv = 1.0f / ltot;
+    if (qi < p.Sq) {
+      T* Ob = static_cast<T*>(p.o) + b * p.os0 + qi * p.os1 + h * p.os2;
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int hd0 = 32 * mt + 8 * i4 + 4 * g;
-        typedef T t4 __attribute__((ext_vector_type(4)));
-        t4 w;
+      for (int mt = 0; mt < MT; ++mt)
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = from_f32<T>(oacc[mt][4 * i4 + e] * inv);
-        *reinterpret_cast<t4*>(Ob + hd0) = w;
-      }
+        for (int i4 = 0; i4 < 4; ++i4) {
+          const int hd0 = 32 * mt + 8 * i4 + 4 * g;
+          typedef T t4 __attribute__((ext_vector_type(4)));
+          t4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = from_f32<T>(oacc[n][mt][4 * i4 + e] * inv);
+          *reinterpret_cast<t4*>(Ob + hd0) = w;
+        }
+    }
   }
 }
 
@@ -344,19 +458,33 @@ __global__ __launch_bounds__(64) void attn_fwd_f32(AttnArgs p) {
   }
 }
 
-template <typename T, int HD, int NW>
+// Work-group shape per head_dim: NW waves of QG x 32 queries. Overridable at build time.
+#ifndef MI355_ATTN_NW64
+#define MI355_ATTN_NW64 8
+#endif
+#ifndef MI355_ATTN_QG64
+#define MI355_ATTN_QG64 1
+#endif
+#ifndef MI355_ATTN_NW128
+#define MI355_ATTN_NW128 8
+#endif
+#ifndef MI355_ATTN_QG128
+#define MI355_ATTN_QG128 1
+#endif
+
+template <typename T, int HD, int NW, int QG>
 int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
   AttnArgs a = a0;
-  constexpr int BM = NW * 32;
+  constexpr int BM = NW * 32 * QG;
   a.n_qtiles = static_cast<int>((a.Sq + BM - 1) / BM);
   dim3 grid(a.n_qtiles, static_cast<unsigned>(a.H), static_cast<unsigned>(a.B));
   dim3 block(NW * 64);
   if (causal) {
-    if (kmask) hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, true, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, true, false>), grid, block, 0, s, a);
+    if (kmask) hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, true, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, true, false>), grid, block, 0, s, a);
   } else {
-    if (kmask) hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, false, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, false, false>), grid, block, 0, s, a);
+    if (kmask) hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, false, true>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, false, false>), grid, block, 0, s, a);
   }
   return static_cast<int>(hipGetLastError());
 }
@@ -393,6 +521,10 @@ extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const voi
     return MI355_E_BAD_SIZE;
   if (head_dim != 64 && head_dim != 128) return MI355_E_HEAD_DIM;
   if (!(scale > 0.f)) return MI355_E_UNSUPPORTED;
+  // per-lane K/V offsets inside a 64-key tile are 32-bit byte offsets
+  if (k_strides[1] <= 0 || v_strides[1] <= 0 || k_strides[1] > ((int64_t)1 << 24) ||
+      v_strides[1] > ((int64_t)1 << 24))
+    return MI355_E_BAD_SIZE;
   // 16-byte row loads (8-byte output stores): strides in elements must keep that alignment.
   const int64_t va = dtype == MI355_F32 ? 4 : 8;
   const int64_t* st[3] = {q_strides, k_strides, v_strides};
@@ -419,7 +551,6 @@ extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const voi
   a.Sq = S_q;
   a.Sk = S_k;
   a.c = scale * 1.4426950408889634f;
-  a.thr = 8.0f / a.c;
   a.kv = key_valid;
   a.kv_sb = key_valid_sb;
   const bool kmask = key_valid != nullptr;
@@ -429,9 +560,11 @@ extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const voi
     return head_dim == 64 ? launch_f32<64>(a, cz, kmask, s) : launch_f32<128>(a, cz, kmask, s);
   }
   if (dtype == MI355_F16) {
-    return head_dim == 64 ? launch_mfma<_Float16, 64, 4>(a, cz, kmask, s)
-                          : launch_mfma<_Float16, 128, 4>(a, cz, kmask, s);
+    return head_dim == 64
+               ? launch_mfma<_Float16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, s)
+               : launch_mfma<_Float16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, s);
   }
-  return head_dim == 64 ? launch_mfma<__bf16, 64, 4>(a, cz, kmask, s)
-                        : launch_mfma<__bf16, 128, 4>(a, cz, kmask, s);
+  return head_dim == 64
+             ? launch_mfma<__bf16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, s)
+             : launch_mfma<__bf16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, s);
 }
