@@ -89,28 +89,35 @@ MI355_DEVINL float frag_sum(bf16x8 f, float acc) {
 // Scores are kept in the log2 domain: the Q fragments are multiplied once by c = scale*log2(e)
 // (re-rounded to the input dtype), and each score MFMA chain starts from a block holding -mu, the
 // running (lazy) max, so the MFMA output is already s*c - mu and feeds v_exp_f32 directly.
-template <typename T, int HD, int NW, int QG, bool CAUSAL, bool KMASK>
-__global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
+template <typename T, int HD, int NW, int QG, int KT, int WPE, bool PRIO, bool PIPE, bool CAUSAL,
+          bool KMASK>
+__global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   constexpr int QW = 32 * QG;   // queries per wave
   constexpr int BM = NW * QW;   // queries per work-group
-  constexpr int BN = 64;        // keys per tile
+  constexpr int BN = 64;        // keys per sub-tile (compute step)
+  constexpr int BS = BN * KT;   // keys per LDS stage (one barrier per stage)
   constexpr int NT = NW * 64;
   constexpr int KCH = HD / 8;   // 16-byte chunks per K row
   constexpr int VCH = BN / 8;   // 16-byte chunks per V^T row
   constexpr int KS = HD / 16;   // MFMA k-steps of S^T
   constexpr int MT = HD / 32;   // 32-row tiles of O^T
-  // loader work: K as 16-byte chunks, V as (key pair, 16-byte chunk) units; threads beyond the
-  // unit count idle in the loader when the work-group is larger than the tile
+  // loader work per sub-tile: K as 16-byte chunks, V as (key pair, 16-byte chunk) units;
+  // threads beyond the unit count idle in the loader when the work-group is larger
   constexpr int K_UNITS_ALL = BN * KCH, V_UNITS_ALL = (BN / 2) * KCH;
   constexpr int K_LOADS = (K_UNITS_ALL + NT - 1) / NT;
   constexpr int V_UNITS = (V_UNITS_ALL + NT - 1) / NT;
   static_assert(K_UNITS_ALL % NT == 0 || NT % K_UNITS_ALL == 0, "K loader shape");
   static_assert(V_UNITS_ALL % NT == 0 || NT % V_UNITS_ALL == 0, "V loader shape");
 
-  __shared__ u32x4 k_lds[2][BN * KCH];
-  __shared__ u32x4 vt_lds[2][HD * VCH];
+  // LDS ring of NSTAGE stages x KT sub-tiles. Without the look-ahead a wave reads one stage
+  // while the loader fills the other (double buffering); with it a wave may read V of sub-tile
+  // j and K of j+1 (two stages), so the loader writes the stage two ahead of a 3-stage ring.
+  constexpr int NSTAGE = PIPE ? 3 : 2;
+  __shared__ u32x4 k_lds[NSTAGE][KT][BN * KCH];
+  __shared__ u32x4 vt_lds[NSTAGE][KT][HD * VCH];
+  __shared__ uint8_t kv_lds[KMASK ? NSTAGE : 1][KMASK ? KT : 1][BN];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
@@ -146,17 +153,18 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
   }
 
   const int64_t kend = CAUSAL ? ((q_wg + BM) < p.Sk ? (q_wg + BM) : p.Sk) : p.Sk;
-  const int n_kt = static_cast<int>((kend + BN - 1) / BN);
+  const int n_kt = static_cast<int>((kend + BN - 1) / BN);   // 64-key sub-tiles
+  const int n_st = (n_kt + KT - 1) / KT;                     // LDS stages
 
   u32x4 rk[K_LOADS], rv0[V_UNITS], rv1[V_UNITS];
-  // key-validity byte of key (tile start + lane), fetched one tile ahead with K/V
-  uint32_t kv_next = 1u, kv_cur = 1u;
+  uint32_t kvr = 1u;
+  // global -> registers for 64-key sub-tile j
   auto load_global = [&](int j) {
     const int k0 = j * BN;
     // tile base in scalar registers, per-lane offsets in 32 bits
     const char* kt = Kb + static_cast<int64_t>(k0) * kstride;
     const char* vt = Vb + static_cast<int64_t>(k0) * vstride;
-    if constexpr (KMASK) kv_next = (k0 + lane < Sk) ? kvb[k0 + lane] : 0u;
+    if constexpr (KMASK) kvr = (k0 + lane < Sk) ? kvb[k0 + lane] : 0u;
 #pragma unroll
     for (int i = 0; i < K_LOADS; ++i) {
       const int idx = tid + i * NT, key = idx / KCH, ch = idx % KCH;
@@ -177,13 +185,17 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
       rv1[i] = c;
     }
   };
-  auto store_lds = [&](int s) {
+  // registers -> LDS stage s, sub-tile slot k
+  auto store_lds = [&](int s, int k) {
+    if constexpr (KMASK) {
+      if (wave == 0) kv_lds[s][k][lane] = static_cast<uint8_t>(kvr != 0u);
+    }
 #pragma unroll
     for (int i = 0; i < K_LOADS; ++i) {
       const int idx = tid + i * NT, key = idx / KCH, ch = idx % KCH;
-      if (idx < K_UNITS_ALL) k_lds[s][key * KCH + (ch ^ swz<KCH>(key))] = rk[i];
+      if (idx < K_UNITS_ALL) k_lds[s][k][key * KCH + (ch ^ swz<KCH>(key))] = rk[i];
     }
-    uint32_t* vt32 = reinterpret_cast<uint32_t*>(&vt_lds[s][0]);
+    uint32_t* vt32 = reinterpret_cast<uint32_t*>(&vt_lds[s][k][0]);
 #pragma unroll
     for (int i = 0; i < V_UNITS; ++i) {
       const int u = tid + i * NT, pr = u % 32, ch = u / 32;
@@ -216,151 +228,216 @@ __global__ __launch_bounds__(NW * 64) void attn_fwd_mfma(AttnArgs p) {
     started[n] = false;
   }
 
-  if (n_kt > 0) {
-    load_global(0);
-    store_lds(0);
+#pragma unroll
+  for (int k = 0; k < (NSTAGE - 1) * KT; ++k) {
+    if (k < n_kt) {
+      load_global(k);
+      store_lds(k / KT, k % KT);
+    }
   }
   __syncthreads();
 
   const int q_wave32 = static_cast<int>(q_wave);
   const float thr = 8.0f;  // log2 units: unnormalised probabilities stay <= 2^8
 
-  auto tile = [&](const int j, const int cur) {
-    if constexpr (KMASK) kv_cur = kv_next;
-    if (j + 1 < n_kt) load_global(j + 1);
-    const int k0 = j * BN;
+  auto kfrag = [&](int st, int k, int t, int s) {
+    const int krow = 32 * t + l32, c = 2 * s + g;
+    return __builtin_bit_cast(frag, k_lds[st][k][krow * KCH + (c ^ swz<KCH>(krow))]);
+  };
+  auto vfrag = [&](int st, int k, int mt, int t, int hh) {
+    const int vrow = 32 * mt + l32, c = 4 * t + 2 * hh + g;
+    return __builtin_bit_cast(frag, vt_lds[st][k][vrow * VCH + (c ^ swz<VCH>(vrow))]);
+  };
+  // causal: a wave whose queries all precede a key tile has nothing to add from it
+  auto active = [&](int j) { return !CAUSAL || j * BN <= q_wave32 + QW - 1; };
 
-    // a wave whose queries all precede this key tile has nothing to add (causal)
-    if (!CAUSAL || k0 <= q_wave32 + QW - 1) {
-      auto kfrag = [&](int t, int s) {
-        const int krow = 32 * t + l32, c = 2 * s + g;
-        return __builtin_bit_cast(frag, k_lds[cur][krow * KCH + (c ^ swz<KCH>(krow))]);
-      };
-      auto vfrag = [&](int mt, int t, int hh) {
-        const int vrow = 32 * mt + l32, c = 4 * t + 2 * hh + g;
-        return __builtin_bit_cast(frag, vt_lds[cur][vrow * VCH + (c ^ swz<VCH>(vrow))]);
-      };
-      // S^T tile (log2 domain, minus mu): 64 keys x QW queries; the K fragments of one 32-key
-      // half are read before its MFMA chain.
-      f32x16 sacc[QG][2];
+  // S^T of sub-tile j (log2 domain, minus mu): 64 keys x QW queries
+  auto score = [&](f32x16 (&sacc)[QG][2], const int st, const int k) {
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
-      for (int t = 0; t < 2; ++t) {
-        frag kf[KS];
+    for (int t = 0; t < 2; ++t) {
+      frag kf[KS];
 #pragma unroll
-        for (int s = 0; s < KS; ++s) kf[s] = kfrag(t, s);
-#pragma unroll
-        for (int n = 0; n < QG; ++n) {
-          sacc[n][t] = MF::mma(kf[0], qf[n][0], negmu[n]);
-#pragma unroll
-          for (int s = 1; s < KS; ++s) sacc[n][t] = MF::mma(kf[s], qf[n][s], sacc[n][t]);
-        }
-      }
-      // with head_dim 64 the whole V^T tile (32 VGPRs per lane) is read ahead of the softmax
-      constexpr bool V_AHEAD = (HD == 64);
-      frag vf[V_AHEAD ? MT : 1][2][2];
-      if constexpr (V_AHEAD) {
-#pragma unroll
-        for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int hh = 0; hh < 2; ++hh) vf[mt][t][hh] = vfrag(mt, t, hh);
-      }
-
-      // tile validity word: bit kk set <=> key k0 + kk is valid under the key mask
-      uint64_t vbits = ~0ull;
-      if constexpr (KMASK) vbits = __builtin_amdgcn_ballot_w64(kv_cur != 0u);
-      const bool need_mask =
-          (vbits != ~0ull) || (k0 + BN > Sk) || (CAUSAL && k0 + BN - 1 > q_wave32);
-      if (need_mask) {
-#pragma unroll
-        for (int n = 0; n < QG; ++n) {
-          const int qi = q_wave32 + 32 * n + l32;
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) {
-              const int kk = 32 * t + mfma_row(i, lane);
-              const int key = k0 + kk;
-              bool ok = key < Sk && ((vbits >> kk) & 1ull);
-              if (CAUSAL) ok = ok && key <= qi;
-              if (!ok) sacc[n][t][i] = NEG_INF;
-            }
-        }
-      }
-
-      frag pf[QG][2][2];
+      for (int s = 0; s < KS; ++s) kf[s] = kfrag(st, k, t, s);
 #pragma unroll
       for (int n = 0; n < QG; ++n) {
-        float mx = NEG_INF;
+        sacc[n][t] = MF::mma(kf[0], qf[n][0], negmu[n]);
 #pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sacc[n][t][i]);
-        mx = pair_max(mx);
-        // move mu only when the tile max exceeds it by more than thr (or on the first finite tile)
-        const bool grow = started[n] ? (mx > thr) : (mx != NEG_INF);
-        if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-          const float shift = grow ? mx : 0.f;
-          const float alpha = started[n] ? fast_exp2(-shift) : 1.f;
-          lsum[n] *= alpha;
-#pragma unroll
-          for (int t = 0; t < MT; ++t)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) oacc[n][t][i] *= alpha;
-#pragma unroll
-          for (int t = 0; t < 2; ++t)
-#pragma unroll
-            for (int i = 0; i < 16; ++i) sacc[n][t][i] -= shift;
-#pragma unroll
-          for (int i = 0; i < 16; ++i) negmu[n][i] -= shift;
-          started[n] = started[n] || grow;
-        }
-#pragma unroll
-        for (int t = 0; t < 2; ++t) {
-          float pv[16];
-#pragma unroll
-          for (int i = 0; i < 16; ++i) pv[i] = fast_exp2(sacc[n][t][i]);
-          pf[n][t][0] = pack8<T>(pv);
-          pf[n][t][1] = pack8<T>(pv + 8);
-          lsum[n] = frag_sum(pf[n][t][0], lsum[n]);
-          lsum[n] = frag_sum(pf[n][t][1], lsum[n]);
-        }
-      }
-
-      // O^T (hd x QW) += V^T (hd x 64 keys) . P^T (64 keys x QW)
-#pragma unroll
-      for (int mt = 0; mt < MT; ++mt) {
-        frag vm[2][2];
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh) {
-            if constexpr (V_AHEAD)
-              vm[t][hh] = vf[mt][t][hh];
-            else
-              vm[t][hh] = vfrag(mt, t, hh);
-          }
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int hh = 0; hh < 2; ++hh)
-#pragma unroll
-            for (int n = 0; n < QG; ++n) oacc[n][mt] = MF::mma(vm[t][hh], pf[n][t][hh], oacc[n][mt]);
+        for (int s = 1; s < KS; ++s) sacc[n][t] = MF::mma(kf[s], qf[n][s], sacc[n][t]);
       }
     }
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
+  };
 
-    if (j + 1 < n_kt) store_lds(cur ^ 1);
+  // masks and the lazy running max of sub-tile j; returns after any O/l/mu update
+  auto softmax_max = [&](f32x16 (&sacc)[QG][2], const int j, const int st, const int k) {
+    const int k0 = j * BN;
+    // tile validity word: bit kk set <=> key k0 + kk is valid under the key mask
+    uint64_t vbits = ~0ull;
+    if constexpr (KMASK) vbits = __builtin_amdgcn_ballot_w64(kv_lds[st][k][lane] != 0);
+    const bool need_mask =
+        (vbits != ~0ull) || (k0 + BN > Sk) || (CAUSAL && k0 + BN - 1 > q_wave32);
+    if (need_mask) {
+#pragma unroll
+      for (int n = 0; n < QG; ++n) {
+        const int qi = q_wave32 + 32 * n + l32;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            const int kk = 32 * t + mfma_row(i, lane);
+            const int key = k0 + kk;
+            bool ok = key < Sk && ((vbits >> kk) & 1ull);
+            if (CAUSAL) ok = ok && key <= qi;
+            if (!ok) sacc[n][t][i] = NEG_INF;
+          }
+      }
+    }
+#pragma unroll
+    for (int n = 0; n < QG; ++n) {
+      // four independent max3 chains, then combine
+      float m4[4];
+#pragma unroll
+      for (int c = 0; c < 4; ++c) {
+        const int t = c >> 1, i0 = (c & 1) * 8;
+        float m = fmaxf(sacc[n][t][i0], sacc[n][t][i0 + 1]);
+#pragma unroll
+        for (int i = i0 + 2; i < i0 + 8; ++i) m = fmaxf(m, sacc[n][t][i]);
+        m4[c] = m;
+      }
+      float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
+      mx = pair_max(mx);
+      // move mu only when the tile max exceeds it by more than thr (or on the first finite tile)
+      const bool grow = started[n] ? (mx > thr) : (mx != NEG_INF);
+      if (__builtin_amdgcn_ballot_w64(grow) != 0) {
+        const float shift = grow ? mx : 0.f;
+        const float alpha = started[n] ? fast_exp2(-shift) : 1.f;
+        lsum[n] *= alpha;
+#pragma unroll
+        for (int t = 0; t < MT; ++t)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) oacc[n][t][i] *= alpha;
+#pragma unroll
+        for (int t = 0; t < 2; ++t)
+#pragma unroll
+          for (int i = 0; i < 16; ++i) sacc[n][t][i] -= shift;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) negmu[n][i] -= shift;
+        started[n] = started[n] || grow;
+      }
+    }
+  };
+
+  // probabilities of sub-tile j and O^T (hd x QW) += V^T (hd x 64 keys) . P^T (64 keys x QW)
+  auto exp_pv = [&](f32x16 (&sacc)[QG][2], const int st, const int k) {
+    frag pf[QG][2][2];
+#pragma unroll
+    for (int n = 0; n < QG; ++n) {
+      float part[4];
+#pragma unroll
+      for (int t = 0; t < 2; ++t) {
+        float pv[16];
+#pragma unroll
+        for (int i = 0; i < 16; ++i) pv[i] = fast_exp2(sacc[n][t][i]);
+        pf[n][t][0] = pack8<T>(pv);
+        pf[n][t][1] = pack8<T>(pv + 8);
+        part[2 * t] = frag_sum(pf[n][t][0], 0.f);
+        part[2 * t + 1] = frag_sum(pf[n][t][1], 0.f);
+      }
+      lsum[n] += (part[0] + part[1]) + (part[2] + part[3]);
+    }
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int mt = 0; mt < MT; ++mt) {
+      frag vm[2][2];
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh) vm[t][hh] = vfrag(st, k, mt, t, hh);
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+          for (int n = 0; n < QG; ++n) oacc[n][mt] = MF::mma(vm[t][hh], pf[n][t][hh], oacc[n][mt]);
+    }
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
+  };
+
+  // S^T of a sub-tile from K fragments already in registers
+  auto score_regs = [&](f32x16 (&sacc)[QG][2], const frag (&kf)[2][KS]) {
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int t = 0; t < 2; ++t)
+#pragma unroll
+      for (int n = 0; n < QG; ++n) {
+        sacc[n][t] = MF::mma(kf[t][0], qf[n][0], negmu[n]);
+#pragma unroll
+        for (int s = 1; s < KS; ++s) sacc[n][t] = MF::mma(kf[t][s], qf[n][s], sacc[n][t]);
+      }
+    if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
+  };
+
+  f32x16 s_a[QG][2], s_b[QG][2];  // s_b is dead without the look-ahead
+  if constexpr (PIPE) {
+    if (n_kt > 0 && active(0)) score(s_a, 0, 0);
+  }
+
+  // one LDS stage (ring slot cur): KT sub-tiles; the sub-tiles of the stage NSTAGE-1 ahead are
+  // fetched before each sub-tile is processed and stored after it (into slot far), then one
+  // barrier. (cur, nxt, far: ring slots of this stage, the next one and the one being filled;
+  // par: parity of its first sub-tile, which selects the score buffer; all are literals after
+  // unrolling)
+  auto stage = [&](const int st, const int cur, const int nxt, const int far, const int par) {
+#pragma unroll
+    for (int k = 0; k < KT; ++k) {
+      const int j = st * KT + k, jf = j + (NSTAGE - 1) * KT;
+      f32x16 (&s_cur)[QG][2] = PIPE && ((k + par) & 1) ? s_b : s_a;
+      f32x16 (&s_nxt)[QG][2] = PIPE && ((k + par) & 1) ? s_a : s_b;
+      if (jf < n_kt) load_global(jf);
+      if constexpr (PIPE) {
+        // Look-ahead: the K fragments of sub-tile j+1 are read first, the max/rescale of
+        // sub-tile j runs while they land, then the score MFMAs of j+1 are issued (with the
+        // updated -mu) and overlap the exponentials and P.V MFMAs of j.
+        if (j < n_kt) {
+          const bool nxt_on = j + 1 < n_kt && active(j + 1);
+          const int nst = (k + 1 < KT) ? cur : nxt, nk = (k + 1 < KT) ? k + 1 : 0;
+          frag kf[2][KS];
+          if (nxt_on) {
+#pragma unroll
+            for (int t = 0; t < 2; ++t)
+#pragma unroll
+              for (int s2 = 0; s2 < KS; ++s2) kf[t][s2] = kfrag(nst, nk, t, s2);
+          }
+          if (active(j)) softmax_max(s_cur, j, cur, k);
+          if (nxt_on) score_regs(s_nxt, kf);
+          if (active(j)) exp_pv(s_cur, cur, k);
+        }
+      } else {
+        if (j < n_kt && active(j)) {
+          score(s_a, cur, k);
+          softmax_max(s_a, j, cur, k);
+          exp_pv(s_a, cur, k);
+        }
+      }
+      if (jf < n_kt) store_lds(far, k);
+    }
     __syncthreads();
   };
 
-  // two tiles per trip: the LDS stage of each is a compile-time constant
-  int j = 0;
-  for (; j + 1 < n_kt; j += 2) {
-    tile(j, 0);
-    tile(j + 1, 1);
+  // U stages per trip (a multiple of the ring depth, with an even sub-tile count when the score
+  // buffers alternate) so every ring slot and buffer choice is a compile-time constant
+  constexpr int U = PIPE ? ((KT % 2 == 0) ? 3 : 6) : NSTAGE;
+  int st = 0;
+  for (; st + U - 1 < n_st; st += U) {
+#pragma unroll
+    for (int u = 0; u < U; ++u)
+      stage(st + u, u % NSTAGE, (u + 1) % NSTAGE, (u + NSTAGE - 1) % NSTAGE, (u * KT) & 1);
   }
-  if (j < n_kt) tile(j, 0);
+#pragma unroll
+  for (int u = 0; u < U - 1; ++u)
+    if (st + u < n_st)
+      stage(st + u, u % NSTAGE, (u + 1) % NSTAGE, (u + NSTAGE - 1) % NSTAGE, (u * KT) & 1);
 
 #pragma unroll
   for (int n = 0; n < QG; ++n) {
@@ -472,6 +549,34 @@ __global__ __launch_bounds__(64) void attn_fwd_f32(AttnArgs p) {
 #define MI355_ATTN_QG128 1
 #endif
 
+// LDS stage = KT 64-key sub-tiles (HD 64, KT 2: 64 KB double-buffered)
+#ifndef MI355_ATTN_KT64
+#define MI355_ATTN_KT64 2
+#endif
+#ifndef MI355_ATTN_KT128
+#define MI355_ATTN_KT128 1
+#endif
+#ifndef MI355_ATTN_WPE
+#define MI355_ATTN_WPE 1
+#endif
+#ifndef MI355_ATTN_PRIO
+#define MI355_ATTN_PRIO 0
+#endif
+// score look-ahead (software pipeline) for unmasked head_dim 64; measured no faster on gfx950
+// than the double-buffered loop, so off by default
+#ifndef MI355_ATTN_PIPE64
+#define MI355_ATTN_PIPE64 0
+#endif
+
+template <typename T, int HD, int NW, int QG, bool CAUSAL, bool KMASK>
+void launch_one(const AttnArgs& a, dim3 grid, dim3 block, hipStream_t s) {
+  constexpr int KT = HD == 64 ? MI355_ATTN_KT64 : MI355_ATTN_KT128;
+  constexpr int WPE = MI355_ATTN_WPE;
+  constexpr bool PRIO = MI355_ATTN_PRIO != 0;
+  constexpr bool PIPE = HD == 64 && !KMASK && MI355_ATTN_PIPE64 != 0;
+  hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, KT, WPE, PRIO, PIPE, CAUSAL, KMASK>), grid, block, 0, s, a);
+}
+
 template <typename T, int HD, int NW, int QG>
 int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
   AttnArgs a = a0;
@@ -480,11 +585,11 @@ int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
   dim3 grid(a.n_qtiles, static_cast<unsigned>(a.H), static_cast<unsigned>(a.B));
   dim3 block(NW * 64);
   if (causal) {
-    if (kmask) hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, true, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, true, false>), grid, block, 0, s, a);
+    if (kmask) launch_one<T, HD, NW, QG, true, true>(a, grid, block, s);
+    else launch_one<T, HD, NW, QG, true, false>(a, grid, block, s);
   } else {
-    if (kmask) hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, false, true>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, false, false>), grid, block, 0, s, a);
+    if (kmask) launch_one<T, HD, NW, QG, false, true>(a, grid, block, s);
+    else launch_one<T, HD, NW, QG, false, false>(a, grid, block, s);
   }
   return static_cast<int>(hipGetLastError());
 }
