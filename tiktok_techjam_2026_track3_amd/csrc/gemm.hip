@@ -5,6 +5,8 @@
 // read per lane. Work-group tile BM x BN, waves arranged WM x WN, each wave owning
 // (BM/WM) x (BN/WN) as 32x32 MFMA tiles. K is staged 128 bytes per row per step (64 fp16,
 // 128 int8, 32 fp32 elements), double-buffered in LDS with an XOR swizzle on 16-byte chunks.
+// The MFMA computes C^T blocks so each lane holds runs of 4 consecutive output features; the
+// epilogue stages the finished tile in LDS and writes it back in 16-byte row chunks.
 #include "common.h"
 
 namespace {
@@ -64,8 +66,14 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
   constexpr int A_LOADS = BM * CH / NT, B_LOADS = BN * CH / NT;
   static_assert((BM * CH) % NT == 0 && (BN * CH) % NT == 0, "loader shape");
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
+  // Output tile staged in LDS for coalesced 16-byte stores (row pitch padded by 16 bytes).
+  constexpr int C_PITCH = BN * static_cast<int>(sizeof(TO)) + 16;
+  constexpr int STAGE_BYTES = 2 * (BM + BN) * CH * 16;
+  constexpr bool STAGE_C = BM * C_PITCH <= 160 * 1024 - 1024;
+  constexpr int LDS_BYTES = (STAGE_C && BM * C_PITCH > STAGE_BYTES) ? BM * C_PITCH : STAGE_BYTES;
 
-  __shared__ u32x4 lds[2][(BM + BN) * CH];
+  __shared__ u32x4 lds_raw[LDS_BYTES / 16];
+  u32x4 (*lds)[(BM + BN) * CH] = reinterpret_cast<u32x4 (*)[(BM + BN) * CH]>(lds_raw);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -112,6 +120,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
     }
   };
 
+  // acc[a][b] holds the 32x32 block (features wn*WTN + 32b .., tokens wm*WTM + 32a ..) as
+  // D = W_rows . A_rows^T: lane l keeps token l%32 and features mfma_row(i, l).
   acc_t acc[TM][TN];
 #pragma unroll
   for (int a = 0; a < TM; ++a)
@@ -136,53 +146,89 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int a = 0; a < TM; ++a) {
         const int row = wm * WTM + a * 32 + l32;
-        u32x4 v = lds[cur][row * CH + (c ^ swz8(row))];
-        fa[a] = __builtin_bit_cast(frag, v);
+        fa[a] = __builtin_bit_cast(frag, lds[cur][row * CH + (c ^ swz8(row))]);
       }
 #pragma unroll
       for (int b = 0; b < TN; ++b) {
         const int row = wn * WTN + b * 32 + l32;
-        u32x4 v = lds[cur][(BM + row) * CH + (c ^ swz8(row))];
-        fb[b] = __builtin_bit_cast(frag, v);
+        fb[b] = __builtin_bit_cast(frag, lds[cur][(BM + row) * CH + (c ^ swz8(row))]);
       }
 #pragma unroll
       for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int b = 0; b < TN; ++b) acc[a][b] = MF::mma(fa[a], fb[b], acc[a][b]);
+        for (int b = 0; b < TN; ++b) acc[a][b] = MF::mma(fb[b], fa[a], acc[a][b]);
     }
     if (kt + 1 < nk) store_lds(cur ^ 1);
     __syncthreads();
   }
 
-  // Epilogue: lane holds column n = l32 of each 32x32 tile and 16 rows (mfma_row).
+  // ---- epilogue: per element bias / dequantisation / row mask, rounded once to TO
+  char* cl = reinterpret_cast<char*>(lds_raw);
 #pragma unroll
-  for (int b = 0; b < TN; ++b) {
-    const int64_t n = n0 + wn * WTN + b * 32 + l32;
-    if (n >= p.N) continue;
-    const float bias_n = p.bias ? p.bias[n] : 0.f;
-    float sw_n = 0.f;
-    if constexpr (INT8) sw_n = p.s_w[n];
+  for (int a = 0; a < TM; ++a) {
+    const int m_loc = wm * WTM + a * 32 + l32;
+    const int64_t m = m0 + m_loc;
+    const bool in_m = m < p.M;
+    const bool valid = !in_m || p.row_valid == nullptr || p.row_valid[m] != 0;
+    float sa_m = 0.f;
+    if constexpr (INT8) sa_m = in_m ? p.s_a[m] : 0.f;
 #pragma unroll
-    for (int a = 0; a < TM; ++a) {
+    for (int b = 0; b < TN; ++b) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int64_t m = m0 + wm * WTM + a * 32 + mfma_row(i, lane);
-        if (m >= p.M) continue;
-        const bool valid = p.row_valid == nullptr || p.row_valid[m] != 0;
-        if constexpr (INT8) {
-          const int32_t raw = acc[a][b][i];
-          if (p.acc_out) p.acc_out[m * p.N + n] = raw;
-          if (p.C) {
+      for (int i4 = 0; i4 < 4; ++i4) {
+        const int n_loc = wn * WTN + b * 32 + 8 * i4 + 4 * g;  // 4 consecutive features
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int64_t n = n0 + n_loc + e;
+          const bool in_n = n < p.N;
+          const float bias_n = (p.bias && in_n) ? p.bias[n] : 0.f;
+          if constexpr (INT8) {
+            const int32_t raw = acc[a][b][4 * i4 + e];
+            if (p.acc_out && in_m && in_n) p.acc_out[m * p.N + n] = raw;
             // y = fp32(acc) * (s_a * s_w) + b, each operation rounded separately (no FMA).
-            float v = static_cast<float>(raw) * (p.s_a[m] * sw_n);
-            if (p.bias) v = v + bias_n;
-            if (!valid) v = 0.f;
-            store_out<TO>(p.C, m * p.ldc + n, v);
+            float y = static_cast<float>(raw) * (sa_m * (in_n ? p.s_w[n] : 0.f));
+            if (p.bias) y = y + bias_n;
+            v[e] = y;
+          } else {
+            v[e] = acc[a][b][4 * i4 + e] + bias_n;
           }
+          if (!valid) v[e] = 0.f;
+        }
+        if constexpr (STAGE_C) {
+          typedef TO to4 __attribute__((ext_vector_type(4)));
+          to4 w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = from_f32<TO>(v[e]);
+          *reinterpret_cast<to4*>(cl + m_loc * C_PITCH + n_loc * static_cast<int>(sizeof(TO))) = w;
         } else {
-          float v = acc[a][b][i] + bias_n;
-          if (!valid) v = 0.f;
-          store_out<TO>(p.C, m * p.ldc + n, v);
+          if (p.C && in_m) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e)
+              if (n0 + n_loc + e < p.N) store_out<TO>(p.C, m * p.ldc + n0 + n_loc + e, v[e]);
+          }
+        }
+      }
+    }
+  }
+  if constexpr (STAGE_C) {
+    __syncthreads();
+    if (p.C) {
+      // coalesced copy of the staged tile: 16-byte chunks, rows of BN outputs
+      constexpr int CPR = BN * static_cast<int>(sizeof(TO)) / 16;  // chunks per row
+      constexpr int EPC_OUT = 16 / static_cast<int>(sizeof(TO));
+      const bool vec_ok = (p.ldc % EPC_OUT) == 0 && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0);
+      for (int idx = tid; idx < BM * CPR; idx += NT) {
+        const int r = idx / CPR, c = idx % CPR;
+        const int64_t m = m0 + r, n = n0 + static_cast<int64_t>(c) * EPC_OUT;
+        if (m >= p.M || n >= p.N) continue;
+        const u32x4 chunk = *reinterpret_cast<const u32x4*>(cl + r * C_PITCH + c * 16);
+        TO* dst = static_cast<TO*>(p.C) + m * p.ldc + n;
+        if (vec_ok && n + EPC_OUT <= p.N) {
+          *reinterpret_cast<u32x4*>(dst) = chunk;
+        } else {
+          const TO* src = reinterpret_cast<const TO*>(&chunk);
+          for (int e = 0; e < EPC_OUT && n + e < p.N; ++e) dst[e] = src[e];
         }
       }
     }
@@ -200,6 +246,14 @@ int launch_gemm(const GemmArgs& a, hipStream_t stream) {
 }
 
 }  // namespace
+
+// 16-bit / int8 work-group tile 256 x 256; wave grid overridable at build time
+#ifndef MI355_GEMM_WM
+#define MI355_GEMM_WM 2
+#endif
+#ifndef MI355_GEMM_WN
+#define MI355_GEMM_WN 4
+#endif
 
 template <typename T, int BM, int BN, int WM, int WN, bool INT8>
 int launch_by_out(const GemmArgs& a, hipStream_t s) {
@@ -240,8 +294,8 @@ extern "C" int mi355_gemm_bias(int in_dtype, int out_dtype, const void* A, int64
   a.out_dtype = out_dtype;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (in_dtype) {
-    case MI355_F16: return launch_by_out<_Float16, 256, 128, 2, 2, false>(a, s);
-    case MI355_BF16: return launch_by_out<__bf16, 256, 128, 2, 2, false>(a, s);
+    case MI355_F16: return launch_by_out<_Float16, 256, 256, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
+    case MI355_BF16: return launch_by_out<__bf16, 256, 256, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
     default: return launch_gemm<float, float, 128, 128, 2, 2, false>(a, s);
   }
 }
@@ -274,5 +328,5 @@ extern "C" int mi355_gemm_i8(const int8_t* A, const int8_t* W, const float* s_a,
   a.N = N;
   a.K = K;
   a.out_dtype = out_dtype;
-  return launch_by_out<int8_t, 256, 128, 2, 2, true>(a, static_cast<hipStream_t>(stream));
+  return launch_by_out<int8_t, 256, 256, MI355_GEMM_WM, MI355_GEMM_WN, true>(a, static_cast<hipStream_t>(stream));
 }
