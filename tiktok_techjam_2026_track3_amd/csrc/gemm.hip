@@ -53,7 +53,10 @@ MI355_DEVINL void tile_coords(int64_t pid, int64_t ntm, int64_t ntn, int64_t& tm
   tn = w / gsize;
 }
 
-template <typename T, typename TO, int BM, int BN, int WM, int WN, bool INT8>
+// DIRECT: K stages are fetched with global_load_lds_dwordx4 (64 lanes x 16 bytes land at
+// M0 + 16*lane), so no registers or ds_write instructions carry the tiles. Requires
+// K % BK == 0; rows beyond M / N are clamped to the last valid row (their results are dropped).
+template <typename T, typename TO, int BM, int BN, int WM, int WN, bool INT8, bool DIRECT>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
@@ -130,15 +133,51 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[a][b][i] = 0;
 
+  // direct loads: wave w issues blocks w, w + NW, ... of 8 rows (1 KB); lane = (row r, chunk pc)
+  constexpr int NWAVE = WM * WN;
+  constexpr int BLOCKS = (BM + BN) / 8;
+  static_assert(BLOCKS % NWAVE == 0, "direct loader shape");
+  static_assert(BM % 16 == 0, "B rows keep the swizzle phase of their stage row");
+  auto load_direct = [&](int s, int64_t k0) {
+    const int r = lane >> 3, pc = lane & 7;
+#pragma unroll
+    for (int i = 0; i < BLOCKS / NWAVE; ++i) {
+      const int blk = wave + i * NWAVE;
+      const int row = blk * 8 + r;                      // row within the A|B stage
+      const int c = pc ^ swz8(row);                     // logical chunk that belongs here
+      const char* src;
+      if (row < BM) {
+        int64_t gm = m0 + row;
+        gm = gm < p.M ? gm : p.M - 1;
+        src = Ab + (gm * p.lda + k0 + c * EPC) * ES;
+      } else {
+        int64_t gn = n0 + (row - BM);
+        gn = gn < p.N ? gn : p.N - 1;
+        src = Wb + (gn * p.ldw + k0 + c * EPC) * ES;
+      }
+      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(&lds[s][blk * 8 * CH]), 16, 0, 0);
+    }
+  };
+
   const int nk = static_cast<int>((p.K + BK - 1) / BK);
-  load_global(0);
-  store_lds(0);
+  if constexpr (DIRECT) {
+    load_direct(0, 0);
+    __builtin_amdgcn_s_waitcnt(0);
+  } else {
+    load_global(0);
+    store_lds(0);
+  }
   __syncthreads();
 
   const int g = lane >> 5, l32 = lane & 31;
   for (int kt = 0; kt < nk; ++kt) {
     const int cur = kt & 1;
-    if (kt + 1 < nk) load_global(static_cast<int64_t>(kt + 1) * BK);
+    if (kt + 1 < nk) {
+      if constexpr (DIRECT)
+        load_direct(cur ^ 1, static_cast<int64_t>(kt + 1) * BK);
+      else
+        load_global(static_cast<int64_t>(kt + 1) * BK);
+    }
 #pragma unroll
     for (int j = 0; j < CH / 2; ++j) {
       const int c = 2 * j + g;
@@ -158,7 +197,11 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
 #pragma unroll
         for (int b = 0; b < TN; ++b) acc[a][b] = MF::mma(fb[b], fa[a], acc[a][b]);
     }
-    if (kt + 1 < nk) store_lds(cur ^ 1);
+    if constexpr (DIRECT) {
+      __builtin_amdgcn_s_waitcnt(0);  // this wave's stage-(kt+1) loads have landed in LDS
+    } else {
+      if (kt + 1 < nk) store_lds(cur ^ 1);
+    }
     __syncthreads();
   }
 
@@ -235,13 +278,21 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
   }
 }
 
+#ifndef MI355_GEMM_DIRECT
+#define MI355_GEMM_DIRECT 1
+#endif
+
 template <typename T, typename TO, int BM, int BN, int WM, int WN, bool INT8>
 int launch_gemm(const GemmArgs& a, hipStream_t stream) {
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (tiles <= 0) return MI355_OK;
   if (tiles > 0x7fffffffLL) return MI355_E_BAD_SIZE;
-  hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8>), dim3(static_cast<unsigned>(tiles)),
-                     dim3(WM * WN * 64), 0, stream, a);
+  constexpr int64_t BK = CH * Mfma<T>::ELEMS_PER_CHUNK;
+  const dim3 grid(static_cast<unsigned>(tiles)), block(WM * WN * 64);
+  if (MI355_GEMM_DIRECT && a.K % BK == 0)
+    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, true>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, false>), grid, block, 0, stream, a);
   return static_cast<int>(hipGetLastError());
 }
 
