@@ -278,18 +278,27 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
     const bool need_mask =
         (vbits != ~0ull) || (k0 + BN > Sk) || (CAUSAL && k0 + BN - 1 > q_wave32);
     if (need_mask) {
+      // one validity word per lane: key mask, sequence end and (causal) the query's diagonal;
+      // shifted by the lane's 4g offset, element (t, i) is bit 32t + 8(i/4) + i%4 -- a
+      // compile-time position, so no per-element shift amounts stay live in registers
+      const int rem = Sk - k0;  // keys left in the sequence (> 0 for an issued sub-tile)
+      uint64_t w = vbits;
+      if (rem < BN) w &= (1ull << rem) - 1ull;
 #pragma unroll
       for (int n = 0; n < QG; ++n) {
-        const int qi = q_wave32 + 32 * n + l32;
+        uint64_t wn = w;
+        if constexpr (CAUSAL) {
+          const int lim = q_wave32 + 32 * n + l32 - k0 + 1;  // keys kk < lim are allowed
+          wn &= lim >= BN ? ~0ull : (lim <= 0 ? 0ull : ((1ull << lim) - 1ull));
+        }
+        const uint64_t wl = wn >> (4 * g);
+        const uint32_t half[2] = {static_cast<uint32_t>(wl), static_cast<uint32_t>(wl >> 32)};
 #pragma unroll
         for (int t = 0; t < 2; ++t)
 #pragma unroll
           for (int i = 0; i < 16; ++i) {
-            const int kk = 32 * t + mfma_row(i, lane);
-            const int key = k0 + kk;
-            bool ok = key < Sk && ((vbits >> kk) & 1ull);
-            if (CAUSAL) ok = ok && key <= qi;
-            if (!ok) sacc[n][t][i] = NEG_INF;
+            const uint32_t bit = 1u << (8 * (i / 4) + (i % 4));
+            if (!(half[t] & bit)) sacc[n][t][i] = NEG_INF;
           }
       }
     }

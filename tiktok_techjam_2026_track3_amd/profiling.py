@@ -1,0 +1,159 @@
+"""Summaries of rocprofv3 CSV output for this library's kernels.
+
+Three reports, each printed as a short text table (the files under ``profiles/`` are these
+reports with the commands that produced them):
+
+* ``stats DIR``   -- per-kernel launch statistics from ``--kernel-trace --stats`` output
+  (``*_kernel_stats.csv``): calls, average / min / max duration, share of GPU time.
+* ``pmc DIR``     -- per-kernel per-dispatch averages of every counter in a ``--pmc`` run
+  (``*_counter_collection.csv``).
+* ``traffic``     -- HBM bytes per launch of one kernel from a ``FETCH_SIZE`` run and a
+  ``WRITE_SIZE`` run, each scaled by the factor that makes the same counter read exactly the
+  known bytes of a plain copy kernel (``bench.py --copy-calibration``), written as JSON.
+
+Usage::
+
+    python -m tiktok_techjam_2026_track3_amd.profiling stats gpurun_out/prof_C2
+    python -m tiktok_techjam_2026_track3_amd.profiling pmc gpurun_out/fetch_C2
+    python -m tiktok_techjam_2026_track3_amd.profiling traffic --config C2 --kernel attn_fwd_mfma \\
+        --fetch gpurun_out/fetch_C2 --write gpurun_out/write_C2 \\
+        --copy-fetch gpurun_out/fetch_copy --copy-write gpurun_out/write_copy --copy-bytes N
+"""
+from __future__ import annotations
+
+import argparse
+import csv
+import glob
+import json
+import os
+import re
+import sys
+from collections import defaultdict
+from typing import Dict, List
+
+_OURS = re.compile(r"(gemm_kernel|attn_fwd_mfma|attn_fwd_f32|quant_rows_kernel)(I[^(]*)?")
+COPY_KERNEL = "neg_kernel"  # the calibration kernel: y = -x, reads and writes every byte once
+
+
+def short_name(name: str) -> str:
+    m = _OURS.search(name)
+    if m:
+        return (m.group(1) + "<" + (m.group(2) or "")[1:] + ">")[:80]
+    m = re.search(r"at::native::[^<(]*?(\w+_kernel\w*)", name)
+    if m:
+        return ("torch " + m.group(1))[:80]
+    return name[:80]
+
+
+def _find(d: str, suffix: str) -> List[str]:
+    files = sorted(glob.glob(os.path.join(d, "**", "*" + suffix), recursive=True))
+    if not files:
+        raise FileNotFoundError(f"no *{suffix} under {d}")
+    return files
+
+
+def kernel_stats(d: str) -> List[dict]:
+    rows = []
+    for path in _find(d, "_kernel_stats.csv"):
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                rows.append({"name": r["Name"], "calls": int(r["Calls"]),
+                             "total_ns": float(r["TotalDurationNs"]), "avg_ns": float(r["AverageNs"]),
+                             "min_ns": float(r["MinNs"]), "max_ns": float(r["MaxNs"]),
+                             "pct": float(r["Percentage"])})
+    rows.sort(key=lambda r: -r["total_ns"])
+    return rows
+
+
+def counters(d: str) -> Dict[str, Dict[str, List[float]]]:
+    """kernel name -> counter -> per-dispatch values (summed over dimensions of one dispatch)."""
+    per = defaultdict(lambda: defaultdict(float))
+    names = {}
+    for path in _find(d, "_counter_collection.csv"):
+        with open(path, newline="") as f:
+            for r in csv.DictReader(f):
+                key = (path, r["Dispatch_Id"])
+                names[key] = r["Kernel_Name"]
+                per[key][r["Counter_Name"]] += float(r["Counter_Value"])
+    out: Dict[str, Dict[str, List[float]]] = defaultdict(lambda: defaultdict(list))
+    for key, vals in per.items():
+        for c, v in vals.items():
+            out[names[key]][c].append(v)
+    return out
+
+
+def _select(table: Dict[str, Dict[str, List[float]]], pattern: str, counter: str) -> List[float]:
+    vals = [v for name, cs in table.items() if re.search(pattern, name) for v in cs.get(counter, [])]
+    if not vals:
+        raise ValueError(f"no dispatch of a kernel matching {pattern!r} carries {counter}")
+    return vals
+
+
+def _mean(v: List[float]) -> float:
+    return sum(v) / len(v)
+
+
+def print_stats(d: str) -> None:
+    rows = kernel_stats(d)
+    print(f"{'kernel':82s} {'calls':>6s} {'avg_us':>11s} {'min_us':>11s} {'max_us':>11s} {'pct':>6s}")
+    for r in rows[:14]:
+        print(f"{short_name(r['name']):82s} {r['calls']:6d} {r['avg_ns'] / 1e3:11.2f} "
+              f"{r['min_ns'] / 1e3:11.2f} {r['max_ns'] / 1e3:11.2f} {r['pct']:6.1f}")
+
+
+def print_pmc(d: str) -> None:
+    table = counters(d)
+    for name in sorted(table, key=lambda n: short_name(n)):
+        cs = table[name]
+        n = max(len(v) for v in cs.values())
+        vals = ", ".join(f"{c}={_mean(v):.6g}" for c, v in sorted(cs.items()))
+        print(f"{short_name(name)} [{n} dispatches]: {vals}")
+
+
+def traffic(config: str, kernel: str, fetch: str, write: str, copy_fetch: str, copy_write: str,
+            copy_bytes: float) -> dict:
+    """HBM bytes per launch of ``kernel``; FETCH_SIZE / WRITE_SIZE are in KiB per dispatch."""
+    cf = _mean(_select(counters(copy_fetch), COPY_KERNEL, "FETCH_SIZE")) * 1024.0
+    cw = _mean(_select(counters(copy_write), COPY_KERNEL, "WRITE_SIZE")) * 1024.0
+    f_fetch, f_write = copy_bytes / cf, copy_bytes / cw
+    kf = _mean(_select(counters(fetch), kernel, "FETCH_SIZE")) * 1024.0
+    kw = _mean(_select(counters(write), kernel, "WRITE_SIZE")) * 1024.0
+    return {"config": config, "kernel": kernel, "fetch_bytes": kf * f_fetch,
+            "write_bytes": kw * f_write, "bytes_per_launch": kf * f_fetch + kw * f_write,
+            "raw_fetch_kib": kf / 1024.0, "raw_write_kib": kw / 1024.0,
+            "copy_bytes": copy_bytes, "copy_fetch_factor": f_fetch, "copy_write_factor": f_write}
+
+
+def main(argv=None) -> int:
+    ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    sub = ap.add_subparsers(dest="cmd", required=True)
+    s = sub.add_parser("stats")
+    s.add_argument("dir")
+    p = sub.add_parser("pmc")
+    p.add_argument("dir")
+    t = sub.add_parser("traffic")
+    for a in ("config", "kernel", "fetch", "write", "copy-fetch", "copy-write"):
+        t.add_argument("--" + a, required=True)
+    t.add_argument("--copy-bytes", type=float, required=True)
+    t.add_argument("--json-out", help="merge the record into this JSON file (keyed by config)")
+    a = ap.parse_args(argv)
+    if a.cmd == "stats":
+        print_stats(a.dir)
+    elif a.cmd == "pmc":
+        print_pmc(a.dir)
+    else:
+        rec = traffic(a.config, a.kernel, a.fetch, a.write, a.copy_fetch, a.copy_write, a.copy_bytes)
+        print(json.dumps(rec, indent=1))
+        if a.json_out:
+            data = {}
+            if os.path.exists(a.json_out):
+                with open(a.json_out) as f:
+                    data = json.load(f)
+            data[a.config] = rec
+            with open(a.json_out, "w") as f:
+                json.dump(data, f, indent=1, sort_keys=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())
