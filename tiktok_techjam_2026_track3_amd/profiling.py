@@ -31,14 +31,31 @@ import sys
 from collections import defaultdict
 from typing import Dict, List
 
-_OURS = re.compile(r"(gemm_kernel|attn_fwd_mfma|attn_fwd_f32|quant_rows_kernel)(I[^(]*)?")
+_OURS = re.compile(r"(gemm_kernel|attn_fwd_mfma|attn_fwd_f32|quant_rows_kernel)(<[^(]*>|I\w*?EEv)?")
+_MANGLED_ARG = re.compile(r"DF16b|DF16_|Li(-?\d+)E|Lb([01])E|[afhsi]")
+_TYPE = {"DF16b": "bf16", "DF16_": "f16", "a": "i8", "f": "f32", "h": "u8", "s": "i16", "i": "i32"}
 COPY_KERNEL = "neg_kernel"  # the calibration kernel: y = -x, reads and writes every byte once
+
+
+def _template_args(raw: str) -> str:
+    """'<_Float16, 64, true>' or the Itanium-mangled 'IDF16_Li64ELb1EEEv' as 'f16,64,1'."""
+    if raw.startswith("<"):
+        args = [a.strip() for a in raw[1:-1].split(",")]
+        conv = {"float": "f32", "_Float16": "f16", "__bf16": "bf16", "signed char": "i8",
+                "true": "1", "false": "0"}
+        return ",".join(conv.get(a, a) for a in args)
+    out = []
+    for m in _MANGLED_ARG.finditer(raw[1:-3]):
+        tok = m.group(0)
+        out.append(m.group(1) if m.group(1) is not None else
+                   m.group(2) if m.group(2) is not None else _TYPE[tok])
+    return ",".join(out)
 
 
 def short_name(name: str) -> str:
     m = _OURS.search(name)
     if m:
-        return (m.group(1) + "<" + (m.group(2) or "")[1:] + ">")[:80]
+        return f"{m.group(1)}<{_template_args(m.group(2)) if m.group(2) else ''}>"[:80]
     m = re.search(r"at::native::[^<(]*?(\w+_kernel\w*)", name)
     if m:
         return ("torch " + m.group(1))[:80]
