@@ -40,6 +40,12 @@ struct AttnArgs {
 constexpr float NEG_INF = -__builtin_huge_valf();
 
 MI355_DEVINL float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+// IEEE maximum (NaN-propagating): gfx950 v_maximum3_f32, no operand canonicalisation needed
+MI355_DEVINL float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+MI355_DEVINL float pair_maximum(float v) {
+  auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
 
 // Position of key kk (0..63) inside a V^T LDS row: bits 2 and 3 swapped, so the 8 keys a lane
 // group feeds one PV MFMA ({0-3, 8-11} + 4g of each 16-key group) are contiguous.
@@ -215,7 +221,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   f32x16 oacc[QG][MT];
   f32x16 negmu[QG];       // -mu replicated: the starting accumulator of every score chain
   float lsum[QG];
-  bool started[QG];       // a finite tile max has been seen (mu is meaningful)
+  float gate[QG];         // rescale threshold: -inf until a finite tile max was seen, then thr
 #pragma unroll
   for (int n = 0; n < QG; ++n) {
 #pragma unroll
@@ -225,7 +231,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) negmu[n][i] = 0.f;
     lsum[n] = 0.f;
-    started[n] = false;
+    gate[n] = NEG_INF;
   }
 
 #pragma unroll
@@ -304,23 +310,22 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
     }
 #pragma unroll
     for (int n = 0; n < QG; ++n) {
-      // four independent max3 chains, then combine
-      float m4[4];
+      // two v_maximum3 chains of 16 scores (NaN-propagating maximum: no operand quieting)
+      float m2[2];
 #pragma unroll
-      for (int c = 0; c < 4; ++c) {
-        const int t = c >> 1, i0 = (c & 1) * 8;
-        float m = fmaxf(sacc[n][t][i0], sacc[n][t][i0 + 1]);
+      for (int t = 0; t < 2; ++t) {
+        float m = vmax(sacc[n][t][0], sacc[n][t][1]);
 #pragma unroll
-        for (int i = i0 + 2; i < i0 + 8; ++i) m = fmaxf(m, sacc[n][t][i]);
-        m4[c] = m;
+        for (int i = 2; i < 16; ++i) m = vmax(m, sacc[n][t][i]);
+        m2[t] = m;
       }
-      float mx = fmaxf(fmaxf(m4[0], m4[1]), fmaxf(m4[2], m4[3]));
-      mx = pair_max(mx);
-      // move mu only when the tile max exceeds it by more than thr (or on the first finite tile)
-      const bool grow = started[n] ? (mx > thr) : (mx != NEG_INF);
+      const float mx = pair_maximum(vmax(m2[0], m2[1]));
+      // move mu only when the tile max exceeds it by more than thr, or on the first finite
+      // tile (gate is -inf until then)
+      const bool grow = mx > gate[n];
       if (__builtin_amdgcn_ballot_w64(grow) != 0) {
         const float shift = grow ? mx : 0.f;
-        const float alpha = started[n] ? fast_exp2(-shift) : 1.f;
+        const float alpha = gate[n] == NEG_INF ? 1.f : fast_exp2(-shift);
         lsum[n] *= alpha;
 #pragma unroll
         for (int t = 0; t < MT; ++t)
@@ -332,7 +337,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
           for (int i = 0; i < 16; ++i) sacc[n][t][i] -= shift;
 #pragma unroll
         for (int i = 0; i < 16; ++i) negmu[n][i] -= shift;
-        started[n] = started[n] || grow;
+        gate[n] = grow ? thr : gate[n];
       }
     }
   };
