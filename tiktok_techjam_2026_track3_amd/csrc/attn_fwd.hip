@@ -47,18 +47,16 @@ MI355_DEVINL float pair_maximum(float v) {
   return vmax(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
 
-// Position of key kk (0..63) inside a V^T LDS row: bits 2 and 3 swapped, so the 8 keys a lane
-// group feeds one PV MFMA ({0-3, 8-11} + 4g of each 16-key group) are contiguous.
-MI355_DEVINL int vt_pos(int kk) {
-  return (kk & ~15) | (kk & 3) | (((kk >> 3) & 1) << 2) | (((kk >> 2) & 1) << 3);
-}
-
+// XOR swizzle of the 16-byte chunks of K/V LDS rows (NCH chunks per row, row = key). It maps
+// row bits 0..3 onto chunk bits so that both read patterns are free of bank conflicts (checked
+// against 32- and 64-bank models): the K fragment reads (ds_read_b128, 32 keys x one chunk) and
+// the V transpose reads (ds_read_b64_tr_b16, 4 keys x 4 chunks per 32 lanes).
 template <int NCH>
 MI355_DEVINL int swz(int r) {
   if constexpr (NCH >= 16)
-    return r & 15;
+    return ((r & 1) << 2) ^ (((r >> 1) & 1) * 10) ^ ((r >> 2) & 3);
   else
-    return (r & 7) ^ ((r >> 3) & 1);
+    return ((r & 1) << 1) ^ ((r & 2) << 1) ^ ((r >> 2) & 3);
 }
 
 template <typename T>
@@ -105,24 +103,23 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   constexpr int BN = 64;        // keys per sub-tile (compute step)
   constexpr int BS = BN * KT;   // keys per LDS stage (one barrier per stage)
   constexpr int NT = NW * 64;
-  constexpr int KCH = HD / 8;   // 16-byte chunks per K row
-  constexpr int VCH = BN / 8;   // 16-byte chunks per V^T row
+  constexpr int KCH = HD / 8;   // 16-byte chunks per K / V row
+  constexpr int ROWB = HD * 2;  // bytes per K / V row
   constexpr int KS = HD / 16;   // MFMA k-steps of S^T
   constexpr int MT = HD / 32;   // 32-row tiles of O^T
-  // loader work per sub-tile: K as 16-byte chunks, V as (key pair, 16-byte chunk) units;
-  // threads beyond the unit count idle in the loader when the work-group is larger
-  constexpr int K_UNITS_ALL = BN * KCH, V_UNITS_ALL = (BN / 2) * KCH;
-  constexpr int K_LOADS = (K_UNITS_ALL + NT - 1) / NT;
-  constexpr int V_UNITS = (V_UNITS_ALL + NT - 1) / NT;
-  static_assert(K_UNITS_ALL % NT == 0 || NT % K_UNITS_ALL == 0, "K loader shape");
-  static_assert(V_UNITS_ALL % NT == 0 || NT % V_UNITS_ALL == 0, "V loader shape");
+  // loader: one global_load_lds_dwordx4 moves 64 lanes x 16 bytes = RB rows of a tile into
+  // contiguous LDS; a sub-tile of K (and of V) is BLK such blocks, spread over the waves
+  constexpr int RB = 64 / KCH;
+  constexpr int BLK = BN / RB;
+  static_assert(BLK % NW == 0, "loader shape");
 
-  // LDS ring of NSTAGE stages x KT sub-tiles. Without the look-ahead a wave reads one stage
-  // while the loader fills the other (double buffering); with it a wave may read V of sub-tile
-  // j and K of j+1 (two stages), so the loader writes the stage two ahead of a 3-stage ring.
+  // LDS ring of NSTAGE stages x KT sub-tiles, K and V both in their natural [key][hd] layout.
+  // Without the look-ahead a wave reads one stage while the other is in flight (double
+  // buffering); with it a wave may read V of sub-tile j and K of j+1 (two stages), so loads go
+  // to the stage two ahead of a 3-stage ring.
   constexpr int NSTAGE = PIPE ? 3 : 2;
   __shared__ u32x4 k_lds[NSTAGE][KT][BN * KCH];
-  __shared__ u32x4 vt_lds[NSTAGE][KT][HD * VCH];
+  __shared__ u32x4 v_lds[NSTAGE][KT][BN * KCH];
   __shared__ uint8_t kv_lds[KMASK ? NSTAGE : 1][KMASK ? KT : 1][BN];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -162,59 +159,30 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   const int n_kt = static_cast<int>((kend + BN - 1) / BN);   // 64-key sub-tiles
   const int n_st = (n_kt + KT - 1) / KT;                     // LDS stages
 
-  u32x4 rk[K_LOADS], rv0[V_UNITS], rv1[V_UNITS];
   uint32_t kvr = 1u;
-  // global -> registers for 64-key sub-tile j
-  auto load_global = [&](int j) {
+  // global -> LDS slot (s, k) for 64-key sub-tile j, asynchronously (vmcnt). Lane i of a block
+  // lands at LDS block base + 16 i, i.e. row i / KCH, physical chunk i % KCH, so it fetches the
+  // logical chunk that the swizzle places there. Keys past the end are clamped to the last key:
+  // their scores are masked, so their probabilities are exactly 0.
+  auto issue_loads = [&](int j, int s, int k) {
     const int k0 = j * BN;
-    // tile base in scalar registers, per-lane offsets in 32 bits
-    const char* kt = Kb + static_cast<int64_t>(k0) * kstride;
-    const char* vt = Vb + static_cast<int64_t>(k0) * vstride;
     if constexpr (KMASK) kvr = (k0 + lane < Sk) ? kvb[k0 + lane] : 0u;
+    const int r = lane / KCH, pc = lane % KCH;
 #pragma unroll
-    for (int i = 0; i < K_LOADS; ++i) {
-      const int idx = tid + i * NT, key = idx / KCH, ch = idx % KCH;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (idx < K_UNITS_ALL && k0 + key < Sk)
-        v = *reinterpret_cast<const u32x4*>(kt + (static_cast<uint32_t>(key) * kstride + ch * 16u));
-      rk[i] = v;
-    }
-#pragma unroll
-    for (int i = 0; i < V_UNITS; ++i) {
-      const int u = tid + i * NT, pr = u % 32, ch = u / 32;
-      const uint32_t off = static_cast<uint32_t>(2 * pr) * vstride + ch * 16u;
-      u32x4 a = {0u, 0u, 0u, 0u}, c = {0u, 0u, 0u, 0u};
-      if (u < V_UNITS_ALL && k0 + 2 * pr < Sk) a = *reinterpret_cast<const u32x4*>(vt + off);
-      if (u < V_UNITS_ALL && k0 + 2 * pr + 1 < Sk)
-        c = *reinterpret_cast<const u32x4*>(vt + (off + vstride));
-      rv0[i] = a;
-      rv1[i] = c;
+    for (int i = 0; i < BLK / NW; ++i) {
+      const int blk = wave + i * NW;
+      const int row = blk * RB + r;
+      const int key = (k0 + row < Sk) ? k0 + row : Sk - 1;
+      const int c = pc ^ swz<KCH>(row);
+      __builtin_amdgcn_global_load_lds(Kb + static_cast<uint64_t>(key) * kstride + c * 16,
+          (__attribute__((address_space(3))) void*)(&k_lds[s][k][blk * 64]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(Vb + static_cast<uint64_t>(key) * vstride + c * 16,
+          (__attribute__((address_space(3))) void*)(&v_lds[s][k][blk * 64]), 16, 0, 0);
     }
   };
-  // registers -> LDS stage s, sub-tile slot k
-  auto store_lds = [&](int s, int k) {
+  auto store_mask = [&](int s, int k) {
     if constexpr (KMASK) {
       if (wave == 0) kv_lds[s][k][lane] = static_cast<uint8_t>(kvr != 0u);
-    }
-#pragma unroll
-    for (int i = 0; i < K_LOADS; ++i) {
-      const int idx = tid + i * NT, key = idx / KCH, ch = idx % KCH;
-      if (idx < K_UNITS_ALL) k_lds[s][k][key * KCH + (ch ^ swz<KCH>(key))] = rk[i];
-    }
-    uint32_t* vt32 = reinterpret_cast<uint32_t*>(&vt_lds[s][k][0]);
-#pragma unroll
-    for (int i = 0; i < V_UNITS; ++i) {
-      const int u = tid + i * NT, pr = u % 32, ch = u / 32;
-      if (u >= V_UNITS_ALL) continue;
-      const int pos = vt_pos(2 * pr);
-      const int pch = pos >> 3, pw = (pos & 7) >> 1;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const int row = 8 * ch + e;
-        const uint32_t lo = (rv0[i][e >> 1] >> (16 * (e & 1))) & 0xffffu;
-        const uint32_t hi = (rv1[i][e >> 1] >> (16 * (e & 1))) & 0xffffu;
-        vt32[(row * VCH + (pch ^ swz<VCH>(row))) * 4 + pw] = lo | (hi << 16);
-      }
     }
   };
 
@@ -237,10 +205,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
 #pragma unroll
   for (int k = 0; k < (NSTAGE - 1) * KT; ++k) {
     if (k < n_kt) {
-      load_global(k);
-      store_lds(k / KT, k % KT);
+      issue_loads(k, k / KT, k % KT);
+      store_mask(k / KT, k % KT);
     }
   }
+  __builtin_amdgcn_s_waitcnt(0);
   __syncthreads();
 
   const int q_wave32 = static_cast<int>(q_wave);
@@ -250,9 +219,32 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
     const int krow = 32 * t + l32, c = 2 * s + g;
     return __builtin_bit_cast(frag, k_lds[st][k][krow * KCH + (c ^ swz<KCH>(krow))]);
   };
+  // V^T fragment (O^T rows 32 mt.., keys of MFMA step (t, hh)) from the natural V tile with two
+  // ds_read_b64_tr_b16: in each 16-lane group, lane 4e+q addresses key k0+e, hd h0+4q..h0+4q+3,
+  // and lane j receives hd h0+j of keys k0..k0+3. Group G covers hd 16 (G & 1).. of O^T tile mt
+  // and keys 4 (G >> 1).. (+8 for the second read): the key order of the P^T fragments.
+  uint32_t v_off[2][MT];
+  {
+    const int vg = lane >> 4, ve = (lane >> 2) & 3, vq = lane & 3;
+#pragma unroll
+    for (int half = 0; half < 2; ++half)
+#pragma unroll
+      for (int mt = 0; mt < MT; ++mt) {
+        const int row = 4 * (vg >> 1) + ve + 8 * half;
+        const int col = 32 * mt + 16 * (vg & 1) + 4 * vq;
+        v_off[half][mt] = row * ROWB + ((col / 8) ^ swz<KCH>(row)) * 16 + (col % 8) * 2;
+      }
+  }
   auto vfrag = [&](int st, int k, int mt, int t, int hh) {
-    const int vrow = 32 * mt + l32, c = 4 * t + 2 * hh + g;
-    return __builtin_bit_cast(frag, vt_lds[st][k][vrow * VCH + (c ^ swz<VCH>(vrow))]);
+    typedef short s4 __attribute__((ext_vector_type(4)));
+    typedef short s8 __attribute__((ext_vector_type(8)));
+    const char* base = reinterpret_cast<const char*>(&v_lds[st][k][0]) + (32 * t + 16 * hh) * ROWB;
+    const s4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s4*)(base + v_off[0][mt]));
+    const s4 hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) s4*)(base + v_off[1][mt]));
+    const s8 v = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    return __builtin_bit_cast(frag, v);
   };
   // causal: a wave whose queries all precede a key tile has nothing to add from it
   auto active = [&](int j) { return !CAUSAL || j * BN <= q_wave32 + QW - 1; };
@@ -408,7 +400,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
       const int j = st * KT + k, jf = j + (NSTAGE - 1) * KT;
       f32x16 (&s_cur)[QG][2] = PIPE && ((k + par) & 1) ? s_b : s_a;
       f32x16 (&s_nxt)[QG][2] = PIPE && ((k + par) & 1) ? s_a : s_b;
-      if (jf < n_kt) load_global(jf);
+      if (jf < n_kt) issue_loads(jf, far, k);
       if constexpr (PIPE) {
         // Look-ahead: the K fragments of sub-tile j+1 are read first, the max/rescale of
         // sub-tile j runs while they land, then the score MFMAs of j+1 are issued (with the
@@ -434,8 +426,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
           exp_pv(s_a, cur, k);
         }
       }
-      if (jf < n_kt) store_lds(far, k);
+      if (jf < n_kt) store_mask(far, k);
     }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads into slot far have landed
     __syncthreads();
   };
 
