@@ -120,7 +120,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   constexpr int NSTAGE = PIPE ? 3 : 2;
   __shared__ u32x4 k_lds[NSTAGE][KT][BN * KCH];
   __shared__ u32x4 v_lds[NSTAGE][KT][BN * KCH];
-  __shared__ uint8_t kv_lds[KMASK ? NSTAGE : 1][KMASK ? KT : 1][BN];
+  // key-mask bytes of each sub-tile: a 1-byte LDS-DMA load writes each lane's byte
+  // zero-extended into its own dword (LDS base + 4 lane)
+  __shared__ uint32_t kv_lds[KMASK ? NSTAGE : 1][KMASK ? KT : 1][BN];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
@@ -159,14 +161,19 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   const int n_kt = static_cast<int>((kend + BN - 1) / BN);   // 64-key sub-tiles
   const int n_st = (n_kt + KT - 1) / KT;                     // LDS stages
 
-  uint32_t kvr = 1u;
   // global -> LDS slot (s, k) for 64-key sub-tile j, asynchronously (vmcnt). Lane i of a block
   // lands at LDS block base + 16 i, i.e. row i / KCH, physical chunk i % KCH, so it fetches the
   // logical chunk that the swizzle places there. Keys past the end are clamped to the last key:
   // their scores are masked, so their probabilities are exactly 0.
   auto issue_loads = [&](int j, int s, int k) {
     const int k0 = j * BN;
-    if constexpr (KMASK) kvr = (k0 + lane < Sk) ? kvb[k0 + lane] : 0u;
+    if constexpr (KMASK) {
+      // the sub-tile's 64 mask bytes, one per lane, straight into LDS (clamped like the keys;
+      // each lands zero-extended in the dword kv_lds[s][k][lane])
+      if (wave == NW - 1)
+        __builtin_amdgcn_global_load_lds(kvb + ((k0 + lane < Sk) ? k0 + lane : Sk - 1),
+            (__attribute__((address_space(3))) void*)(&kv_lds[s][k][0]), 1, 0, 0);
+    }
     const int r = lane / KCH, pc = lane % KCH;
 #pragma unroll
     for (int i = 0; i < BLK / NW; ++i) {
@@ -178,11 +185,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
           (__attribute__((address_space(3))) void*)(&k_lds[s][k][blk * 64]), 16, 0, 0);
       __builtin_amdgcn_global_load_lds(Vb + static_cast<uint64_t>(key) * vstride + c * 16,
           (__attribute__((address_space(3))) void*)(&v_lds[s][k][blk * 64]), 16, 0, 0);
-    }
-  };
-  auto store_mask = [&](int s, int k) {
-    if constexpr (KMASK) {
-      if (wave == 0) kv_lds[s][k][lane] = static_cast<uint8_t>(kvr != 0u);
     }
   };
 
@@ -206,7 +208,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   for (int k = 0; k < (NSTAGE - 1) * KT; ++k) {
     if (k < n_kt) {
       issue_loads(k, k / KT, k % KT);
-      store_mask(k / KT, k % KT);
     }
   }
   __builtin_amdgcn_s_waitcnt(0);
@@ -426,7 +427,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
           exp_pv(s_a, cur, k);
         }
       }
-      if (jf < n_kt) store_mask(far, k);
     }
     __builtin_amdgcn_s_waitcnt(0);  // this wave's loads into slot far have landed
     __syncthreads();
@@ -563,8 +563,13 @@ __global__ __launch_bounds__(64) void attn_fwd_f32(AttnArgs p) {
 #ifndef MI355_ATTN_KT128
 #define MI355_ATTN_KT128 1
 #endif
-#ifndef MI355_ATTN_WPE
-#define MI355_ATTN_WPE 1
+// minimum waves per SIMD the register allocation must allow: head_dim 64 fits 128 VGPRs, so two
+// 8-wave work-groups share a CU (the LDS ring takes 64 KB each); head_dim 128 needs ~250 VGPRs
+#ifndef MI355_ATTN_WPE64
+#define MI355_ATTN_WPE64 4
+#endif
+#ifndef MI355_ATTN_WPE128
+#define MI355_ATTN_WPE128 1
 #endif
 #ifndef MI355_ATTN_PRIO
 #define MI355_ATTN_PRIO 0
@@ -578,7 +583,7 @@ __global__ __launch_bounds__(64) void attn_fwd_f32(AttnArgs p) {
 template <typename T, int HD, int NW, int QG, bool CAUSAL, bool KMASK>
 void launch_one(const AttnArgs& a, dim3 grid, dim3 block, hipStream_t s) {
   constexpr int KT = HD == 64 ? MI355_ATTN_KT64 : MI355_ATTN_KT128;
-  constexpr int WPE = MI355_ATTN_WPE;
+  constexpr int WPE = HD == 64 ? MI355_ATTN_WPE64 : MI355_ATTN_WPE128;
   constexpr bool PRIO = MI355_ATTN_PRIO != 0;
   constexpr bool PIPE = HD == 64 && !KMASK && MI355_ATTN_PIPE64 != 0;
   hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, KT, WPE, PRIO, PIPE, CAUSAL, KMASK>), grid, block, 0, s, a);
