@@ -93,6 +93,10 @@ MI355_DEVINL float frag_sum(bf16x8 f, float acc) {
 // Scores are kept in the log2 domain: the Q fragments are multiplied once by c = scale*log2(e)
 // (re-rounded to the input dtype), and each score MFMA chain starts from a block holding -mu, the
 // running (lazy) max, so the MFMA output is already s*c - mu and feeds v_exp_f32 directly.
+#ifndef MI355_ATTN_NSTAGE
+#define MI355_ATTN_NSTAGE 2
+#endif
+
 template <typename T, int HD, int NW, int QG, int KT, int WPE, bool PRIO, bool PIPE, bool CAUSAL,
           bool KMASK>
 __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
@@ -117,7 +121,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   // Without the look-ahead a wave reads one stage while the other is in flight (double
   // buffering); with it a wave may read V of sub-tile j and K of j+1 (two stages), so loads go
   // to the stage two ahead of a 3-stage ring.
-  constexpr int NSTAGE = PIPE ? 3 : 2;
+  constexpr int NSTAGE = PIPE ? 3 : MI355_ATTN_NSTAGE;
   __shared__ u32x4 k_lds[NSTAGE][KT][BN * KCH];
   __shared__ u32x4 v_lds[NSTAGE][KT][BN * KCH];
   // key-mask bytes of each sub-tile: a 1-byte LDS-DMA load writes each lane's byte

@@ -9,6 +9,11 @@
 // epilogue stages the finished tile in LDS and writes it back in 16-byte row chunks.
 #include "common.h"
 
+// interleave the LDS fragment reads of k-slice j+1 with the MFMAs of slice j (scheduler hints)
+#ifndef MI355_GEMM_SCHED
+#define MI355_GEMM_SCHED 1
+#endif
+
 namespace {
 
 struct GemmArgs {
@@ -178,24 +183,40 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
       else
         load_global(static_cast<int64_t>(kt + 1) * BK);
     }
-#pragma unroll
-    for (int j = 0; j < CH / 2; ++j) {
+    // fragments of k-slice j+1 are read while the MFMAs of slice j run (two register sets)
+    frag fa[2][TM], fb[2][TN];
+    auto read_frags = [&](int j, int buf) {
       const int c = 2 * j + g;
-      frag fa[TM], fb[TN];
 #pragma unroll
       for (int a = 0; a < TM; ++a) {
         const int row = wm * WTM + a * 32 + l32;
-        fa[a] = __builtin_bit_cast(frag, lds[cur][row * CH + (c ^ swz8(row))]);
+        fa[buf][a] = __builtin_bit_cast(frag, lds[cur][row * CH + (c ^ swz8(row))]);
       }
 #pragma unroll
       for (int b = 0; b < TN; ++b) {
         const int row = wn * WTN + b * 32 + l32;
-        fb[b] = __builtin_bit_cast(frag, lds[cur][(BM + row) * CH + (c ^ swz8(row))]);
+        fb[buf][b] = __builtin_bit_cast(frag, lds[cur][(BM + row) * CH + (c ^ swz8(row))]);
       }
+    };
+    read_frags(0, 0);
+#pragma unroll
+    for (int j = 0; j < CH / 2; ++j) {
+      if (j + 1 < CH / 2) read_frags(j + 1, (j + 1) & 1);
 #pragma unroll
       for (int a = 0; a < TM; ++a)
 #pragma unroll
-        for (int b = 0; b < TN; ++b) acc[a][b] = MF::mma(fb[b], fa[a], acc[a][b]);
+        for (int b = 0; b < TN; ++b) acc[a][b] = MF::mma(fb[j & 1][b], fa[j & 1][a], acc[a][b]);
+#if MI355_GEMM_SCHED
+      // issue order: MFMA, LDS read, MFMA, LDS read, ... then the remaining MFMAs
+      if (j + 1 < CH / 2) {
+#pragma unroll
+        for (int i = 0; i < TM + TN; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+          __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+        }
+        __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
+      }
+#endif
     }
     if constexpr (DIRECT) {
       __builtin_amdgcn_s_waitcnt(0);  // this wave's stage-(kt+1) loads have landed in LDS
@@ -300,10 +321,10 @@ int launch_gemm(const GemmArgs& a, hipStream_t stream) {
 
 // 16-bit / int8 work-group tile 256 x 256; wave grid overridable at build time
 #ifndef MI355_GEMM_WM
-#define MI355_GEMM_WM 2
+#define MI355_GEMM_WM 4
 #endif
 #ifndef MI355_GEMM_WN
-#define MI355_GEMM_WN 4
+#define MI355_GEMM_WN 2
 #endif
 
 template <typename T, int BM, int BN, int WM, int WN, bool INT8>
