@@ -7,6 +7,10 @@ with the all-true validity mask the reference's timing loop passes
 (torch_transformer_benchmark.py:529-536). The default workload is configuration C2
 (B8 S2048 d1024 H16x64 fp16, non-causal); ``--config`` selects another (C1..C5, comma list).
 
+Untimed warm-up: ``--warmup`` steps, continued until at least ``--min-warmup-s`` seconds of
+back-to-back steps have run (the GPU's clocks ramp over a few hundred milliseconds), then exactly
+``--steps`` timed steps.
+
 Printed (stdout, one JSON line per configuration): whole-block TFLOP/s and ms/step over the timed
 steps (HIP events on the launch stream, bracketed by device synchronisation), per-kernel averages
 from events recorded around every launch inside the timed region, the roofline of the dominant
@@ -32,8 +36,11 @@ def log(*a):
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=20)
-    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--steps", type=int, default=100)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--min-warmup-s", type=float, default=0.5,
+                    help="keep warming up (untimed) until this many seconds of back-to-back steps "
+                         "have run, so the timed steps see sustained clocks")
     ap.add_argument("--config", default="C2", help="C1..C5 or a comma-separated list")
     ap.add_argument("--cpu-budget", type=float, default=20.0,
                     help="approximate seconds of CPU-oracle work for the cpu_baseline leg")
@@ -150,7 +157,7 @@ def cpu_baseline(w, budget_s: float) -> dict:
 
 
 # ------------------------------------------------------------------------------ gpu measure
-def measure(name: str, steps: int, warmup: int) -> dict:
+def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5) -> dict:
     import torch
     from tiktok_techjam_2026_track3_amd import Int8SelfAttention, SelfAttention
     from tiktok_techjam_2026_track3_amd import workloads as W
@@ -175,9 +182,15 @@ def measure(name: str, steps: int, warmup: int) -> dict:
     events = [{s: torch.cuda.Event(enable_timing=True) for s in marks_order} for _ in range(steps)]
     start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     with torch.inference_mode():
-        for _ in range(warmup):
+        t_w = time.perf_counter()
+        n_warm = 0
+        while n_warm < warmup or time.perf_counter() - t_w < min_warmup_s:
             mod(x, valid, w.causal)
+            n_warm += 1
+            if n_warm % 8 == 0:
+                torch.cuda.synchronize()  # tie the wall clock to the GPU's progress
         torch.cuda.synchronize()
+        warm_s = time.perf_counter() - t_w
         t0 = time.perf_counter()
         start.record()
         for k in range(steps):
@@ -234,6 +247,8 @@ def measure(name: str, steps: int, warmup: int) -> dict:
                      "algorithmic_bytes": by[dom], "dtype": kdt},
         "stages": stage_report,
         "wall_s": round(wall, 3),
+        "warmup_steps_run": n_warm,
+        "warmup_s": round(warm_s, 3),
     }
     return result
 
@@ -260,7 +275,7 @@ def main() -> int:
             log(f"unknown config {name}")
             return 2
         log(f"[bench] {name}: warmup {args.warmup}, steps {args.steps}")
-        res = measure(name, args.steps, args.warmup)
+        res = measure(name, args.steps, args.warmup, args.min_warmup_s)
         log(f"[bench] {name}: {res['ms_per_step']} ms/step, {res['value']} {res['unit']}")
         if not args.no_cpu_baseline:
             log(f"[bench] {name}: cpu baseline (budget {args.cpu_budget}s)")
