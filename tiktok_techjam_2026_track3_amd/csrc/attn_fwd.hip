@@ -39,6 +39,25 @@ struct AttnArgs {
 
 constexpr float NEG_INF = -__builtin_huge_valf();
 
+// Work-group -> (query tile, head, batch). Non-causal grids are (q tiles, H, B). Causal grids are
+// 1-D and issued longest-first over the whole launch: every (batch, head)'s last query tile, then
+// every second-to-last one, ... (a query tile's work grows with its index), so no long tile is
+// left for the end. Consecutive work-groups are different heads; those of one head are H*B apart.
+template <bool CAUSAL>
+MI355_DEVINL void tile_of_block(const AttnArgs& p, int& qt, int64_t& h, int64_t& b) {
+  if constexpr (CAUSAL) {
+    const int64_t lin = blockIdx.x, hb_n = p.H * p.B;
+    qt = p.n_qtiles - 1 - static_cast<int>(lin / hb_n);
+    const int64_t hb = lin % hb_n;
+    h = hb % p.H;
+    b = hb / p.H;
+  } else {
+    qt = static_cast<int>(blockIdx.x);
+    h = blockIdx.y;
+    b = blockIdx.z;
+  }
+}
+
 MI355_DEVINL float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 // IEEE maximum (NaN-propagating): gfx950 v_maximum3_f32, no operand canonicalisation needed
 MI355_DEVINL float vmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
@@ -115,7 +134,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   // contiguous LDS; a sub-tile of K (and of V) is BLK such blocks, spread over the waves
   constexpr int RB = 64 / KCH;
   constexpr int BLK = BN / RB;
-  static_assert(BLK % NW == 0, "loader shape");
+  static_assert(BLK % NW == 0 || NW % BLK == 0, "loader shape");
 
   // LDS ring of NSTAGE stages x KT sub-tiles, K and V both in their natural [key][hd] layout.
   // Without the look-ahead a wave reads one stage while the other is in flight (double
@@ -130,8 +149,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
-  const int qt = CAUSAL ? (p.n_qtiles - 1 - static_cast<int>(blockIdx.x)) : static_cast<int>(blockIdx.x);
-  const int64_t h = blockIdx.y, b = blockIdx.z;
+  int qt;
+  int64_t h, b;
+  tile_of_block<CAUSAL>(p, qt, h, b);
   const int64_t q_wg = static_cast<int64_t>(qt) * BM;
   const int64_t q_wave = q_wg + wave * QW;  // first query of this wave
 
@@ -180,8 +200,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
     }
     const int r = lane / KCH, pc = lane % KCH;
 #pragma unroll
-    for (int i = 0; i < BLK / NW; ++i) {
+    for (int i = 0; i < (BLK + NW - 1) / NW; ++i) {
       const int blk = wave + i * NW;
+      if (NW > BLK && blk >= BLK) break;  // more waves than blocks: the rest idle here
       const int row = blk * RB + r;
       const int key = (k0 + row < Sk) ? k0 + row : Sk - 1;
       const int c = pc ^ swz<KCH>(row);
@@ -479,8 +500,9 @@ __global__ __launch_bounds__(64) void attn_fwd_f32(AttnArgs p) {
   __shared__ float ks[BN][HD];
   __shared__ float vs[BN][HD];
   const int lane = threadIdx.x;
-  const int qt = CAUSAL ? (p.n_qtiles - 1 - static_cast<int>(blockIdx.x)) : static_cast<int>(blockIdx.x);
-  const int64_t h = blockIdx.y, b = blockIdx.z;
+  int qt;
+  int64_t h, b;
+  tile_of_block<CAUSAL>(p, qt, h, b);
   const int64_t q_wg = static_cast<int64_t>(qt) * 64;
   const int64_t qi = q_wg + lane;
   const float* Qb = static_cast<const float*>(p.q) + b * p.qs0 + h * p.qs2;
@@ -560,12 +582,13 @@ __global__ __launch_bounds__(64) void attn_fwd_f32(AttnArgs p) {
 #define MI355_ATTN_QG128 1
 #endif
 
-// LDS stage = KT 64-key sub-tiles (HD 64, KT 2: 64 KB double-buffered)
+// LDS stage = KT 64-key sub-tiles, double-buffered: head_dim 64 KT 2 = 64 KB (two work-groups
+// per CU), head_dim 128 KT 2 = 128 KB (one work-group per CU, a barrier every 128 keys)
 #ifndef MI355_ATTN_KT64
 #define MI355_ATTN_KT64 2
 #endif
 #ifndef MI355_ATTN_KT128
-#define MI355_ATTN_KT128 1
+#define MI355_ATTN_KT128 2
 #endif
 // minimum waves per SIMD the register allocation must allow: head_dim 64 fits 128 VGPRs, so two
 // 8-wave work-groups share a CU (the LDS ring takes 64 KB each); head_dim 128 needs ~250 VGPRs
@@ -598,8 +621,13 @@ int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
   AttnArgs a = a0;
   constexpr int BM = NW * 32 * QG;
   a.n_qtiles = static_cast<int>((a.Sq + BM - 1) / BM);
+  const dim3 block(NW * 64);
   dim3 grid(a.n_qtiles, static_cast<unsigned>(a.H), static_cast<unsigned>(a.B));
-  dim3 block(NW * 64);
+  if (causal) {
+    const int64_t n = static_cast<int64_t>(a.n_qtiles) * a.H * a.B;
+    if (n * (NW * 64) > 0xffffffffLL) return MI355_E_BAD_SIZE;  // dispatch size is 32-bit
+    grid = dim3(static_cast<unsigned>(n), 1, 1);
+  }
   if (causal) {
     if (kmask) launch_one<T, HD, NW, QG, true, true>(a, grid, block, s);
     else launch_one<T, HD, NW, QG, true, false>(a, grid, block, s);
@@ -616,6 +644,9 @@ int launch_f32(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
   a.n_qtiles = static_cast<int>((a.Sq + 63) / 64);
   dim3 grid(a.n_qtiles, static_cast<unsigned>(a.H), static_cast<unsigned>(a.B));
   if (causal) {
+    const int64_t n = static_cast<int64_t>(a.n_qtiles) * a.H * a.B;
+    if (n * 64 > 0xffffffffLL) return MI355_E_BAD_SIZE;
+    grid = dim3(static_cast<unsigned>(n), 1, 1);
     if (kmask) hipLaunchKernelGGL((attn_fwd_f32<HD, true, true>), grid, dim3(64), 0, s, a);
     else hipLaunchKernelGGL((attn_fwd_f32<HD, true, false>), grid, dim3(64), 0, s, a);
   } else {
