@@ -114,16 +114,18 @@ MI355_DEVINL float pair_sum(float v) {
 MI355_DEVINL int elem_size(int dtype) { return dtype == MI355_F32 ? 4 : 2; }
 
 // Buffer load straight into LDS (buffer_load_dwordx4 ... lds): 16 bytes per lane from
-// base + voffset, landing at LDS lds_base + 16 * lane. The resource covers `bytes` bytes from
-// `base`; dwords past it read as 0. The resource is built in these device functions so its type
+// base + soffset + voffset, landing at LDS lds_base + 16 * lane. The resource covers `bytes` bytes
+// from `base` (the range check includes soffset); dwords past it read as 0. The resource is built in these device functions so its type
 // never appears in host-compiled code.
 MI355_DEVINL __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
                                            0x00020000 /* raw buffer, 32-bit data format */);
 }
-MI355_DEVINL void buffer_load_lds16(const void* base, uint32_t bytes, void* lds_base, uint32_t voffset) {
+MI355_DEVINL void buffer_load_lds16(const void* base, uint32_t bytes, void* lds_base, uint32_t voffset,
+                                    uint32_t soffset = 0) {
   __builtin_amdgcn_raw_ptr_buffer_load_lds(raw_rsrc(base, bytes),
-                                           (__attribute__((address_space(3))) void*)lds_base, 16, voffset, 0, 0, 0);
+                                           (__attribute__((address_space(3))) void*)lds_base, 16, voffset,
+                                           soffset, 0, 0);
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }

@@ -138,29 +138,39 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
 #pragma unroll
       for (int i = 0; i < 16; ++i) acc[a][b][i] = 0;
 
-  // direct loads: wave w issues blocks w, w + NW, ... of 8 rows (1 KB); lane = (row r, chunk pc)
+  // direct loads (buffer loads to LDS): wave w issues blocks w, w + NW, ... of 8 rows (1 KB);
+  // lane = (row r, physical chunk pc) fetches the logical chunk the swizzle places there. Each
+  // lane's byte offset is fixed across K steps and the step advances the scalar offset; the
+  // A / W resources start at the tile's first row and end at row M / N, so rows past the end
+  // read as zeros (their results are never stored).
   constexpr int NWAVE = WM * WN;
   constexpr int BLOCKS = (BM + BN) / 8;
-  static_assert(BLOCKS % NWAVE == 0, "direct loader shape");
+  constexpr int NLD = BLOCKS / NWAVE;
+  static_assert(BLOCKS % NWAVE == 0 && (BM / 8) % NWAVE == 0, "direct loader shape");
   static_assert(BM % 16 == 0, "B rows keep the swizzle phase of their stage row");
-  auto load_direct = [&](int s, int64_t k0) {
-    const int r = lane >> 3, pc = lane & 7;
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t a_pitch = static_cast<uint32_t>(p.lda) * ES, w_pitch = static_cast<uint32_t>(p.ldw) * ES;
+  const char* a_base = Ab + m0 * static_cast<int64_t>(a_pitch);
+  const char* w_base = Wb + n0 * static_cast<int64_t>(w_pitch);
+  const uint32_t a_bytes = static_cast<uint32_t>(p.M - m0 < BM ? p.M - m0 : BM) * a_pitch;
+  const uint32_t w_bytes = static_cast<uint32_t>(p.N - n0 < BN ? p.N - n0 : BN) * w_pitch;
+  uint32_t doff[NLD];
 #pragma unroll
-    for (int i = 0; i < BLOCKS / NWAVE; ++i) {
-      const int blk = wave + i * NWAVE;
-      const int row = blk * 8 + r;                      // row within the A|B stage
-      const int c = pc ^ swz8(row);                     // logical chunk that belongs here
-      const char* src;
-      if (row < BM) {
-        int64_t gm = m0 + row;
-        gm = gm < p.M ? gm : p.M - 1;
-        src = Ab + (gm * p.lda + k0 + c * EPC) * ES;
-      } else {
-        int64_t gn = n0 + (row - BM);
-        gn = gn < p.N ? gn : p.N - 1;
-        src = Wb + (gn * p.ldw + k0 + c * EPC) * ES;
-      }
-      __builtin_amdgcn_global_load_lds(src, (__attribute__((address_space(3))) void*)(&lds[s][blk * 8 * CH]), 16, 0, 0);
+  for (int i = 0; i < NLD; ++i) {
+    const int row = (wv + i * NWAVE) * 8 + (lane >> 3);  // row within the A|B stage
+    const int c = (lane & 7) ^ swz8(row);
+    doff[i] = row < BM ? static_cast<uint32_t>(row) * a_pitch + c * 16u
+                       : static_cast<uint32_t>(row - BM) * w_pitch + c * 16u;
+  }
+  auto load_direct = [&](int s, int64_t k0) {
+    const uint32_t so = static_cast<uint32_t>(k0) * ES;
+#pragma unroll
+    for (int i = 0; i < NLD; ++i) {
+      const int blk = wv + i * NWAVE;
+      if (i < (BM / 8) / NWAVE)
+        buffer_load_lds16(a_base, a_bytes, &lds[s][blk * 8 * CH], doff[i], so);
+      else
+        buffer_load_lds16(w_base, w_bytes, &lds[s][blk * 8 * CH], doff[i], so);
     }
   };
 
@@ -310,7 +320,12 @@ int launch_gemm(const GemmArgs& a, hipStream_t stream) {
   if (tiles > 0x7fffffffLL) return MI355_E_BAD_SIZE;
   constexpr int64_t BK = CH * Mfma<T>::ELEMS_PER_CHUNK;
   const dim3 grid(static_cast<unsigned>(tiles)), block(WM * WN * 64);
-  if (MI355_GEMM_DIRECT && a.K % BK == 0)
+  // direct path: K a whole number of steps, and a tile's rows (256 x pitch) addressable with
+  // 32-bit buffer offsets
+  const bool direct = MI355_GEMM_DIRECT && a.K % BK == 0 &&
+                      a.lda * static_cast<int64_t>(sizeof(T)) <= (int64_t{1} << 23) &&
+                      a.ldw * static_cast<int64_t>(sizeof(T)) <= (int64_t{1} << 23);
+  if (direct)
     hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, true>), grid, block, 0, stream, a);
   else
     hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, false>), grid, block, 0, stream, a);
