@@ -235,3 +235,27 @@ def test_gemm_i8_dequant_bit_exact(gpu, out_dtype):
                         out_dtype=out_dtype).cpu()
     want = torch.from_numpy(want32).to(out_dtype)
     assert torch.equal(out, want)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_attention_key_mask_repeatable(gpu, dtype):
+    """The masked case above, repeated: every run must give bit-identical, correct output (a
+    loader variant that reloaded spilled offsets returned wrong rows for one wave now and then)."""
+    ops = _ops()
+    B, S, H, hd = 3, 150, 2, 64
+    g = torch.Generator().manual_seed(5)
+    mask = torch.rand(B, S, generator=g) > 0.25
+    mask[:, 0] = True
+    mask[2] = torch.arange(S) < 77
+    q, k, v = (_rand((B, S, H, hd), dtype, 31 + i).to(gpu) for i in range(3))
+    ref = OA.attention_core(*(t.double().cpu().transpose(1, 2) for t in (q, k, v)), hd ** -0.5,
+                            False, mask).transpose(1, 2)
+    first = None
+    for rep in range(12):
+        out = torch.full((B, S, H, hd), float("nan"), dtype=dtype, device=gpu)
+        ops.attention(q, k, v, out=out, scale=hd ** -0.5, key_valid=mask.to(gpu))
+        o = out.cpu()
+        assert (o.double() - ref).abs().max().item() <= 0.02, f"run {rep}"
+        if first is None:
+            first = o
+        assert torch.equal(o, first), f"run {rep} differs from run 0"

@@ -185,42 +185,31 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   const int n_kt = static_cast<int>((kend + BN - 1) / BN);   // 64-key sub-tiles
   const int n_st = (n_kt + KT - 1) / KT;                     // LDS stages
 
-  // global -> LDS slot (s, k) for 64-key sub-tile j, asynchronously (vmcnt), with buffer loads
-  // to LDS: lane i of a block lands at LDS block base + 16 i, i.e. row i / KCH, physical chunk
-  // i % KCH, so it fetches the logical chunk that the swizzle places there. Each lane's byte
-  // offset inside a sub-tile is fixed (computed once); a sub-tile only rebases the scalar buffer
-  // resource, whose range ends at the last key: rows past the end read as zeros (their scores are
-  // masked, so their probabilities are exactly 0), with no per-lane clamping.
-  constexpr int NBL = (BLK + NW - 1) / NW;  // blocks per wave per sub-tile
-  const int wv = __builtin_amdgcn_readfirstlane(wave);
-  uint32_t koff[NBL], voff[NBL];
-#pragma unroll
-  for (int i = 0; i < NBL; ++i) {
-    const int row = (wv + i * NW) * RB + lane / KCH;
-    const int c = (lane % KCH) ^ swz<KCH>(row);
-    koff[i] = static_cast<uint32_t>(row) * kstride + c * 16u;
-    voff[i] = static_cast<uint32_t>(row) * vstride + c * 16u;
-  }
+  // global -> LDS slot (s, k) for 64-key sub-tile j, asynchronously (vmcnt). Lane i of a block
+  // lands at LDS block base + 16 i, i.e. row i / KCH, physical chunk i % KCH, so it fetches the
+  // logical chunk that the swizzle places there. Keys past the end are clamped to the last key:
+  // their scores are masked, so their probabilities are exactly 0.
   auto issue_loads = [&](int j, int s, int k) {
     const int k0 = j * BN;
-    // rows of this sub-tile inside the sequence (>= 1 for an issued sub-tile); the resource
-    // range covers only them, so it fits 32 bits (64 rows of at most 2^25-byte strides)
-    const uint32_t rem = static_cast<uint32_t>(Sk - k0 < BN ? Sk - k0 : BN);
     if constexpr (KMASK) {
-      // the sub-tile's 64 mask bytes, one per lane (clamped like the keys), by a byte-wide LDS
-      // DMA load: each lands zero-extended in the dword kv_lds[s][k][lane]
-      if (wv == NW - 1)
+      // the sub-tile's 64 mask bytes, one per lane, straight into LDS (clamped like the keys;
+      // each lands zero-extended in the dword kv_lds[s][k][lane])
+      if (wave == NW - 1)
         __builtin_amdgcn_global_load_lds(kvb + ((k0 + lane < Sk) ? k0 + lane : Sk - 1),
             (__attribute__((address_space(3))) void*)(&kv_lds[s][k][0]), 1, 0, 0);
     }
-    const char* kb = Kb + k0 * static_cast<uint64_t>(kstride);
-    const char* vb = Vb + k0 * static_cast<uint64_t>(vstride);
+    const int r = lane / KCH, pc = lane % KCH;
 #pragma unroll
-    for (int i = 0; i < NBL; ++i) {
-      const int blk = wv + i * NW;
+    for (int i = 0; i < (BLK + NW - 1) / NW; ++i) {
+      const int blk = wave + i * NW;
       if (NW > BLK && blk >= BLK) break;  // more waves than blocks: the rest idle here
-      buffer_load_lds16(kb, rem * kstride, &k_lds[s][k][blk * 64], koff[i]);
-      buffer_load_lds16(vb, rem * vstride, &v_lds[s][k][blk * 64], voff[i]);
+      const int row = blk * RB + r;
+      const int key = (k0 + row < Sk) ? k0 + row : Sk - 1;
+      const int c = pc ^ swz<KCH>(row);
+      __builtin_amdgcn_global_load_lds(Kb + static_cast<uint64_t>(key) * kstride + c * 16,
+          (__attribute__((address_space(3))) void*)(&k_lds[s][k][blk * 64]), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(Vb + static_cast<uint64_t>(key) * vstride + c * 16,
+          (__attribute__((address_space(3))) void*)(&v_lds[s][k][blk * 64]), 16, 0, 0);
     }
   };
 

@@ -37,8 +37,27 @@ MI355_DEVINL void store_out(void* C, int64_t idx, float v) {
 
 constexpr int CH = 8;  // 16-byte chunks per LDS row per K step (128 bytes)
 
-// Chunk swizzle: conflict-free 16-byte fragment reads for 8- or 16-lane LDS phases.
+// Chunk swizzles (XOR of the 16-byte chunk index by row bits): conflict-free fragment reads
+// (32 rows x one chunk per instruction) for 8-chunk (128-byte) and 4-chunk (64-byte) rows, checked
+// against 32- and 64-bank LDS models.
 MI355_DEVINL int swz8(int r) { return (r & 7) ^ ((r >> 3) & 1); }
+template <int NCH>
+MI355_DEVINL int swzc(int r) {
+  if constexpr (NCH == 8)
+    return swz8(r);
+  else
+    return ((r >> 1) & 3) ^ ((r >> 3) & 1);
+}
+
+// direct (LDS-DMA) path: 16-byte chunks per row per K step, and depth of the LDS ring. Measured
+// on the projection shapes: 8 chunks x 2 stages beats 4 chunks x 3-4 stages (the shorter K step
+// doubles the barriers per tile)
+#ifndef MI355_GEMM_CHD
+#define MI355_GEMM_CHD 8
+#endif
+#ifndef MI355_GEMM_NST
+#define MI355_GEMM_NST 2
+#endif
 
 // XCD-aware work-group order: the dispatcher deals work-groups round-robin to the 8 XCDs, so
 // hand each XCD a contiguous range of logical tiles (shared A rows / W columns stay in its L2),
@@ -58,9 +77,10 @@ MI355_DEVINL void tile_coords(int64_t pid, int64_t ntm, int64_t ntn, int64_t& tm
   tn = w / gsize;
 }
 
-// DIRECT: K stages are fetched with global_load_lds_dwordx4 (64 lanes x 16 bytes land at
-// M0 + 16*lane), so no registers or ds_write instructions carry the tiles. Requires
-// K % BK == 0; rows beyond M / N are clamped to the last valid row (their results are dropped).
+// DIRECT: K steps are fetched with buffer loads to LDS (64 lanes x 16 bytes land at
+// M0 + 16*lane), so no registers or ds_write instructions carry the tiles, into a ring of NST
+// slots of CHK chunks per row. Requires K % BK == 0. Otherwise a register-staged, double-
+// buffered loader with bounds checks runs (8 chunks per row).
 template <typename T, typename TO, int BM, int BN, int WM, int WN, bool INT8, bool DIRECT>
 __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
   using MF = Mfma<T>;
@@ -68,7 +88,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
   using acc_t = typename MF::acc;
   constexpr int NT = WM * WN * 64;
   constexpr int EPC = MF::ELEMS_PER_CHUNK;
-  constexpr int BK = CH * EPC;
+  constexpr int CHK = DIRECT ? MI355_GEMM_CHD : CH;  // 16-byte chunks per row per K step
+  constexpr int NST = DIRECT ? MI355_GEMM_NST : 2;   // LDS ring depth
+  static_assert(CHK == 4 || CHK == 8, "chunks per row");
+  constexpr int BK = CHK * EPC;
   constexpr int WTM = BM / WM, WTN = BN / WN;
   constexpr int TM = WTM / 32, TN = WTN / 32;
   constexpr int A_LOADS = BM * CH / NT, B_LOADS = BN * CH / NT;
@@ -76,12 +99,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
   static_assert(WTM % 32 == 0 && WTN % 32 == 0, "wave tile");
   // Output tile staged in LDS for coalesced 16-byte stores (row pitch padded by 16 bytes).
   constexpr int C_PITCH = BN * static_cast<int>(sizeof(TO)) + 16;
-  constexpr int STAGE_BYTES = 2 * (BM + BN) * CH * 16;
+  constexpr int STAGE_BYTES = NST * (BM + BN) * CHK * 16;
   constexpr bool STAGE_C = BM * C_PITCH <= 160 * 1024 - 1024;
   constexpr int LDS_BYTES = (STAGE_C && BM * C_PITCH > STAGE_BYTES) ? BM * C_PITCH : STAGE_BYTES;
 
   __shared__ u32x4 lds_raw[LDS_BYTES / 16];
-  u32x4 (*lds)[(BM + BN) * CH] = reinterpret_cast<u32x4 (*)[(BM + BN) * CH]>(lds_raw);
+  u32x4 (*lds)[(BM + BN) * CHK] = reinterpret_cast<u32x4 (*)[(BM + BN) * CHK]>(lds_raw);
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int wm = wave / WN, wn = wave % WN;
@@ -144,9 +167,10 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
   // A / W resources start at the tile's first row and end at row M / N, so rows past the end
   // read as zeros (their results are never stored).
   constexpr int NWAVE = WM * WN;
-  constexpr int BLOCKS = (BM + BN) / 8;
-  constexpr int NLD = BLOCKS / NWAVE;
-  static_assert(BLOCKS % NWAVE == 0 && (BM / 8) % NWAVE == 0, "direct loader shape");
+  constexpr int RBK = 64 / CHK;            // rows per 1 KB block
+  constexpr int BLOCKS = (BM + BN) / RBK;
+  constexpr int NLD = BLOCKS / NWAVE;      // loads per wave per K step
+  static_assert(BLOCKS % NWAVE == 0 && (BM / RBK) % NWAVE == 0, "direct loader shape");
   static_assert(BM % 16 == 0, "B rows keep the swizzle phase of their stage row");
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const uint32_t a_pitch = static_cast<uint32_t>(p.lda) * ES, w_pitch = static_cast<uint32_t>(p.ldw) * ES;
@@ -157,8 +181,8 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
   uint32_t doff[NLD];
 #pragma unroll
   for (int i = 0; i < NLD; ++i) {
-    const int row = (wv + i * NWAVE) * 8 + (lane >> 3);  // row within the A|B stage
-    const int c = (lane & 7) ^ swz8(row);
+    const int row = (wv + i * NWAVE) * RBK + lane / CHK;  // row within the A|B stage
+    const int c = (lane % CHK) ^ swzc<CHK>(row);
     doff[i] = row < BM ? static_cast<uint32_t>(row) * a_pitch + c * 16u
                        : static_cast<uint32_t>(row - BM) * w_pitch + c * 16u;
   }
@@ -167,58 +191,44 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
 #pragma unroll
     for (int i = 0; i < NLD; ++i) {
       const int blk = wv + i * NWAVE;
-      if (i < (BM / 8) / NWAVE)
-        buffer_load_lds16(a_base, a_bytes, &lds[s][blk * 8 * CH], doff[i], so);
+      if (i < (BM / RBK) / NWAVE)
+        buffer_load_lds16(a_base, a_bytes, &lds[s][blk * 64], doff[i], so);
       else
-        buffer_load_lds16(w_base, w_bytes, &lds[s][blk * 8 * CH], doff[i], so);
+        buffer_load_lds16(w_base, w_bytes, &lds[s][blk * 64], doff[i], so);
     }
   };
 
   const int nk = static_cast<int>((p.K + BK - 1) / BK);
-  if constexpr (DIRECT) {
-    load_direct(0, 0);
-    __builtin_amdgcn_s_waitcnt(0);
-  } else {
-    load_global(0);
-    store_lds(0);
-  }
-  __syncthreads();
-
   const int g = lane >> 5, l32 = lane & 31;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) {
-      if constexpr (DIRECT)
-        load_direct(cur ^ 1, static_cast<int64_t>(kt + 1) * BK);
-      else
-        load_global(static_cast<int64_t>(kt + 1) * BK);
-    }
-    // fragments of k-slice j+1 are read while the MFMAs of slice j run (two register sets)
+
+  // MFMAs of one K step from ring slot `cur`; the fragments of k-slice j+1 are read while the
+  // MFMAs of slice j run (two register sets)
+  auto compute = [&](const int cur) {
     frag fa[2][TM], fb[2][TN];
     auto read_frags = [&](int j, int buf) {
       const int c = 2 * j + g;
 #pragma unroll
       for (int a = 0; a < TM; ++a) {
         const int row = wm * WTM + a * 32 + l32;
-        fa[buf][a] = __builtin_bit_cast(frag, lds[cur][row * CH + (c ^ swz8(row))]);
+        fa[buf][a] = __builtin_bit_cast(frag, lds[cur][row * CHK + (c ^ swzc<CHK>(row))]);
       }
 #pragma unroll
       for (int b = 0; b < TN; ++b) {
         const int row = wn * WTN + b * 32 + l32;
-        fb[buf][b] = __builtin_bit_cast(frag, lds[cur][(BM + row) * CH + (c ^ swz8(row))]);
+        fb[buf][b] = __builtin_bit_cast(frag, lds[cur][(BM + row) * CHK + (c ^ swzc<CHK>(row))]);
       }
     };
     read_frags(0, 0);
 #pragma unroll
-    for (int j = 0; j < CH / 2; ++j) {
-      if (j + 1 < CH / 2) read_frags(j + 1, (j + 1) & 1);
+    for (int j = 0; j < CHK / 2; ++j) {
+      if (j + 1 < CHK / 2) read_frags(j + 1, (j + 1) & 1);
 #pragma unroll
       for (int a = 0; a < TM; ++a)
 #pragma unroll
         for (int b = 0; b < TN; ++b) acc[a][b] = MF::mma(fb[j & 1][b], fa[j & 1][a], acc[a][b]);
 #if MI355_GEMM_SCHED
       // issue order: MFMA, LDS read, MFMA, LDS read, ... then the remaining MFMAs
-      if (j + 1 < CH / 2) {
+      if (j + 1 < CHK / 2) {
 #pragma unroll
         for (int i = 0; i < TM + TN; ++i) {
           __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
@@ -228,12 +238,59 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
       }
 #endif
     }
-    if constexpr (DIRECT) {
-      __builtin_amdgcn_s_waitcnt(0);  // this wave's stage-(kt+1) loads have landed in LDS
-    } else {
-      if (kt + 1 < nk) store_lds(cur ^ 1);
-    }
+  };
+
+  if constexpr (DIRECT) {
+    // ring of NST slots: step kt computes slot kt % NST while steps kt+1 .. kt+NST-1 are in
+    // flight; before the barrier a wave waits only for its loads of step kt+1
+    constexpr int VM_FULL = (NST - 2) * NLD;  // loads issued after those of step kt+1
+    static_assert(VM_FULL < 64, "vmcnt range");
+    // s_waitcnt immediate: vmcnt(VM_FULL), lgkmcnt(0) (no LDS read of the slot refilled next may
+    // still be in flight), expcnt not waited
+    constexpr int WAIT_FULL = (VM_FULL & 15) | ((VM_FULL >> 4) << 14) | (7 << 4);
+    // Work-group barrier without __syncthreads()'s release fence, which would wait for every
+    // outstanding LDS-DMA load and so drain the ring; the explicit s_waitcnt before it provides
+    // exactly the ordering needed, and the empty asm statements keep the compiler from moving
+    // memory operations across it.
+    auto ring_barrier = [] {
+      asm volatile("" ::: "memory");
+      __builtin_amdgcn_s_barrier();
+      asm volatile("" ::: "memory");
+    };
+#pragma unroll
+    for (int st = 0; st < NST - 1; ++st)
+      if (st < nk) load_direct(st, static_cast<int64_t>(st) * BK);
+    __builtin_amdgcn_s_waitcnt(0);
     __syncthreads();
+    auto step = [&](const int kt, const int slot) {
+      const int kl = kt + NST - 1;
+      if (kl < nk) load_direct((slot + NST - 1) % NST, static_cast<int64_t>(kl) * BK);
+      compute(slot);
+      if (kl < nk)
+        __builtin_amdgcn_s_waitcnt(WAIT_FULL);
+      else
+        __builtin_amdgcn_s_waitcnt(0);
+      ring_barrier();
+    };
+    int kt = 0;
+    for (; kt + NST <= nk; kt += NST) {
+#pragma unroll
+      for (int u = 0; u < NST; ++u) step(kt + u, u);
+    }
+#pragma unroll
+    for (int u = 0; u < NST - 1; ++u)
+      if (kt + u < nk) step(kt + u, u);
+  } else {
+    load_global(0);
+    store_lds(0);
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      const int cur = kt & 1;
+      if (kt + 1 < nk) load_global(static_cast<int64_t>(kt + 1) * BK);
+      compute(cur);
+      if (kt + 1 < nk) store_lds(cur ^ 1);
+      __syncthreads();
+    }
   }
 
   // ---- epilogue: per element bias / dequantisation / row mask, rounded once to TO
@@ -318,7 +375,7 @@ int launch_gemm(const GemmArgs& a, hipStream_t stream) {
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (tiles <= 0) return MI355_OK;
   if (tiles > 0x7fffffffLL) return MI355_E_BAD_SIZE;
-  constexpr int64_t BK = CH * Mfma<T>::ELEMS_PER_CHUNK;
+  constexpr int64_t BK = MI355_GEMM_CHD * Mfma<T>::ELEMS_PER_CHUNK;  // K step of the direct path
   const dim3 grid(static_cast<unsigned>(tiles)), block(WM * WN * 64);
   // direct path: K a whole number of steps, and a tile's rows (256 x pitch) addressable with
   // 32-bit buffer offsets
