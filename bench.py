@@ -45,6 +45,11 @@ def parse_args():
     ap.add_argument("--cpu-budget", type=float, default=20.0,
                     help="approximate seconds of CPU-oracle work for the cpu_baseline leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--attention-half", action="store_true",
+                    help="time the block's whole attention half instead, x + attention(norm1(x)) "
+                         "(torch_transformer_benchmark.py:139): LayerNorm kernel, QKV projection, "
+                         "attention, out projection with the residual add in its epilogue "
+                         "(16-bit / fp32 configurations)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain copy kernel (y = -x, fp16) over BYTES bytes, three times; "
                          "profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE it calibrates the "
@@ -157,7 +162,8 @@ def cpu_baseline(w, budget_s: float) -> dict:
 
 
 # ------------------------------------------------------------------------------ gpu measure
-def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5) -> dict:
+def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
+            half: bool = False) -> dict:
     import torch
     from tiktok_techjam_2026_track3_amd import Int8SelfAttention, SelfAttention
     from tiktok_techjam_2026_track3_amd import workloads as W
@@ -165,6 +171,8 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5) -> di
     w = W.CONFIGS[name]
     dev = torch.device("cuda:0")
     params = W.make_params(w)
+    if half and w.int8:
+        raise ValueError("--attention-half covers the 16-bit / fp32 configurations")
     if w.int8:
         mod = Int8SelfAttention(w.d_model, w.heads)
         mod.load_state_dict(params)
@@ -177,6 +185,15 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5) -> di
         stages = ["qkv", "attn", "out"]
     x = W.make_input(w, W.TIMING_SEED, device="cuda")
     valid = torch.ones(w.batch, w.seq, dtype=torch.bool, device=dev)
+    if half:
+        norm = torch.nn.LayerNorm(w.d_model).to(device=dev, dtype=w.dtype)
+        stages = ["norm"] + stages
+
+        def step(marks=None):
+            return mod.forward_residual(x, norm, valid, w.causal, marks=marks)
+    else:
+        def step(marks=None):
+            return mod.run(x, valid, w.causal, marks=marks)
 
     marks_order = stages + ["end"]
     events = [{s: torch.cuda.Event(enable_timing=True) for s in marks_order} for _ in range(steps)]
@@ -185,7 +202,7 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5) -> di
         t_w = time.perf_counter()
         n_warm = 0
         while n_warm < warmup or time.perf_counter() - t_w < min_warmup_s:
-            mod(x, valid, w.causal)
+            step()
             n_warm += 1
             if n_warm % 8 == 0:
                 torch.cuda.synchronize()  # tie the wall clock to the GPU's progress
@@ -195,13 +212,31 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5) -> di
         start.record()
         for k in range(steps):
             ev = events[k]
-            mod.run(x, valid, w.causal, marks=lambda s, ev=ev: ev[s].record())
+            step(marks=lambda s, ev=ev: ev[s].record())
         end.record()
         torch.cuda.synchronize()
         wall = time.perf_counter() - t0
+        unfused_ms = None
+        if half:
+            # the same half as three separate passes: torch LayerNorm, the block, torch add
+            # (warmed up first: the first torch launches of a shape load their kernels)
+            for _ in range(max(3, warmup // 4)):
+                x + mod.run(norm(x), valid, w.causal)
+            torch.cuda.synchronize()
+            u0, u1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            u0.record()
+            for _ in range(steps):
+                x + mod.run(norm(x), valid, w.causal)
+            u1.record()
+            torch.cuda.synchronize()
+            unfused_ms = u0.elapsed_time(u1) / steps
     ms_step = start.elapsed_time(end) / steps
     fl = w.flops()
-    by = w.bytes()
+    by = dict(w.bytes())
+    if half:
+        act = w.tokens * w.d_model * x.element_size()
+        by["norm"] = 2 * act                      # read x, write norm1(x)
+        by["out"] = by["out"] + act               # the residual read in the epilogue
     stage_ms = {}
     for i, s in enumerate(stages):
         nxt = marks_order[i + 1]
@@ -238,7 +273,9 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5) -> di
         "vs_baseline": None,
         "dtype": ("int8+fp16" if w.int8 else ("bf16 projections, fp16 SDPA core" if w.dtype == torch.bfloat16 else dt)),
         "data": "synthetic (seeded N(0,1) inputs, configuration weight init)",
-        "config": {"workload": f"{w.name}: {w.description}", "batch": w.batch, "seq_len": w.seq,
+        "config": {"workload": f"{w.name}: {w.description}"
+                               + (" + norm1 and residual (attention half of the block)" if half else ""),
+                   "batch": w.batch, "seq_len": w.seq,
                    "d_model": w.d_model, "heads": w.heads, "head_dim": w.head_dim,
                    "causal": w.causal, "parallelism": "none (1 GPU)"},
         "roofline": {"kernel": kernel_name, "bound": "mfma", "achieved": round(achieved, 2),
@@ -247,6 +284,7 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5) -> di
                      "algorithmic_bytes": by[dom], "dtype": kdt},
         "stages": stage_report,
         "wall_s": round(wall, 3),
+        **({"unfused_half_ms_per_step": round(unfused_ms, 5)} if unfused_ms is not None else {}),
         "warmup_steps_run": n_warm,
         "warmup_s": round(warm_s, 3),
     }
@@ -275,7 +313,7 @@ def main() -> int:
             log(f"unknown config {name}")
             return 2
         log(f"[bench] {name}: warmup {args.warmup}, steps {args.steps}")
-        res = measure(name, args.steps, args.warmup, args.min_warmup_s)
+        res = measure(name, args.steps, args.warmup, args.min_warmup_s, args.attention_half)
         log(f"[bench] {name}: {res['ms_per_step']} ms/step, {res['value']} {res['unit']}")
         if not args.no_cpu_baseline:
             log(f"[bench] {name}: cpu baseline (budget {args.cpu_budget}s)")

@@ -109,6 +109,32 @@ int mi355_gemm_i8(const int8_t* A, const int8_t* W, const float* s_a, const floa
                   const float* bias, int out_dtype, void* C, int64_t ldc, int32_t* acc_out,
                   int64_t M, int64_t N, int64_t K, const uint8_t* row_valid, void* stream);
 
+/*
+ * Row LayerNorm: Y[m,:] = (X[m,:] - mean) * rstd * gamma + beta over the last dimension (K), with
+ * fp32 mean, biased variance and rstd = 1 / sqrt(var + eps), Y rounded once to dtype. Replaces
+ * `self.norm1(x)` of BaselineTransformerBlock.forward (torch_transformer_benchmark.py:139;
+ * nn.LayerNorm(d_model), :128), the input of the attention block. dtype F32/F16/BF16 for X, Y,
+ * gamma and beta (gamma/beta nullable: 1 / 0, as elementwise_affine=False). K % (16 / sizeof(elem))
+ * == 0, K <= 8192 (16-bit) / 4096 (fp32), 16-byte aligned pointers; Y may equal X (in place).
+ */
+int mi355_layernorm(int dtype, const void* X, int64_t ldx, const void* gamma, const void* beta,
+                    float eps, void* Y, int64_t ldy, int64_t M, int64_t K, void* stream);
+
+/*
+ * Projection with the block's residual add fused into its epilogue:
+ *   C = R + out_dtype(A · W^T + bias)
+ * i.e. `x + self.attention(...)` of BaselineTransformerBlock.forward
+ * (torch_transformer_benchmark.py:139) with the attention's out_proj (:118) and its output-row
+ * mask (:120-121): the projection is rounded to out_dtype first and the sum rounded again (the
+ * reference adds two tensors of that dtype); rows with row_valid[m] == 0 give C = R (the masked
+ * attention row is zero). R has out_dtype and row stride ldr; R may be C (in place). Otherwise as
+ * mi355_gemm_bias.
+ */
+int mi355_gemm_bias_residual(int in_dtype, int out_dtype, const void* A, int64_t lda, const void* W,
+                             int64_t ldw, const float* bias, const void* R, int64_t ldr, void* C,
+                             int64_t ldc, int64_t M, int64_t N, int64_t K, const uint8_t* row_valid,
+                             void* stream);
+
 #ifdef __cplusplus
 }
 #endif

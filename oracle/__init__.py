@@ -5,8 +5,9 @@ import this package, and only as the checker (or the timed CPU baseline). The pr
 (``tiktok_techjam_2026_track3_amd``) never imports it and has no CPU fallback.
 
 Contents (each function cites the reference file:line it restates):
-  attention.py  dense fp32 torch-CPU restatement of ``BaselineSelfAttention.forward`` and an
-                fp64 numpy brute force used to pin it;
+  attention.py  dense fp32 torch-CPU restatement of ``BaselineSelfAttention.forward``, of the
+                block's LayerNorm and of its attention half ``x + attention(norm1(x))``, and
+                fp64 numpy brute forces used to pin them;
   streamed.py   chunk-wise online-softmax restatement of ``streamed_attention``;
   int8.py       numpy restatement of the W8A8 recipe (``_quant_rows``, ``_int8_pack``,
                 ``_int8_linear``) with exact integer GEMM;
@@ -17,6 +18,10 @@ Contents (each function cites the reference file:line it restates):
 How each function is pinned (the reference ships no golden vectors for this path):
   attention.self_attention     fp64 brute force (per-row loops) + closed-form special cases
   attention.attention_core     same, plus softmax shift/permutation invariances
+  attention.layer_norm         fp64 brute force, torch.nn.functional.layer_norm, closed forms
+                               (constant row -> bias, two-element row -> -+1, shift/scale
+                               invariance), planted-mistake checks
+  attention.attention_half     fp64 brute force of norm + attention + residual
   streamed.*                   equals the dense restatement (fp32 reassociation only)
   int8.quant_rows / pack       hand-computed cases: zero row, row max -> +-127, .5 ties to even
   int8.int8_gemm               brute-force int64 loops on small shapes

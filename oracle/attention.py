@@ -83,9 +83,67 @@ def qkv_projection(x: torch.Tensor, params: Dict[str, torch.Tensor]) -> torch.Te
     return torch.nn.functional.linear(x.float(), w, b)
 
 
+def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor],
+               eps: float = 1e-5) -> torch.Tensor:
+    """nn.LayerNorm over the last dimension (``norm1`` of torch_transformer_benchmark.py:128,
+    applied at :139) in torch-CPU fp32 (fp64 stays fp64): biased variance, eps inside the
+    square root, then the elementwise affine map."""
+    x = x.to(torch.promote_types(x.dtype, torch.float32))
+    mean = x.mean(-1, keepdim=True)
+    var = ((x - mean) ** 2).mean(-1, keepdim=True)
+    y = (x - mean) / torch.sqrt(var + eps)
+    if weight is not None:
+        y = y * weight.to(y.dtype)
+    if bias is not None:
+        y = y + bias.to(y.dtype)
+    return y
+
+
+def attention_half(x: torch.Tensor, norm_weight: Optional[torch.Tensor],
+                   norm_bias: Optional[torch.Tensor], params: Dict[str, torch.Tensor],
+                   num_heads: int, valid_token_mask: Optional[torch.Tensor] = None,
+                   causal: bool = False, eps: float = 1e-5,
+                   round_to: Optional[torch.dtype] = None) -> torch.Tensor:
+    """``x + attention(norm1(x), valid_token_mask, causal)``, the first residual branch of
+    BaselineTransformerBlock.forward (torch_transformer_benchmark.py:139), in fp32.
+
+    ``round_to`` applies the roundings of a block run in that dtype: the norm output, the
+    attention output (:118-122, ``.to(x.dtype)`` of the module) and the residual sum are each
+    rounded to it; None keeps every stage fp32.
+    """
+    rnd = (lambda t: t.to(round_to).float()) if round_to is not None else (lambda t: t)
+    xf = x.float()
+    h = rnd(layer_norm(xf, norm_weight, norm_bias, eps))
+    a = rnd(self_attention(h, params, num_heads, valid_token_mask, causal))
+    return rnd(xf + a)
+
+
 # ---------------------------------------------------------------------------------------------
 # fp64 brute force (pins the torch restatement)
 # ---------------------------------------------------------------------------------------------
+
+def layer_norm_bruteforce(x, weight=None, bias=None, eps: float = 1e-5) -> np.ndarray:
+    """Per-row fp64 LayerNorm with explicit loops over the row."""
+    x = np.asarray(x, dtype=np.float64)
+    rows = x.reshape(-1, x.shape[-1])
+    K = rows.shape[1]
+    w = np.ones(K) if weight is None else np.asarray(weight, dtype=np.float64)
+    b = np.zeros(K) if bias is None else np.asarray(bias, dtype=np.float64)
+    out = np.empty_like(rows)
+    for r in range(rows.shape[0]):
+        mean = 0.0
+        for j in range(K):
+            mean += rows[r, j]
+        mean /= K
+        var = 0.0
+        for j in range(K):
+            var += (rows[r, j] - mean) ** 2
+        var /= K
+        inv = 1.0 / np.sqrt(var + eps)
+        for j in range(K):
+            out[r, j] = (rows[r, j] - mean) * inv * w[j] + b[j]
+    return out.reshape(x.shape)
+
 
 def attention_core_bruteforce(q, k, v, scale: float, causal: bool = False, valid=None) -> np.ndarray:
     """Per-query-row fp64 softmax attention on [B, H, S, hd] arrays."""

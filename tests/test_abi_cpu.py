@@ -74,6 +74,33 @@ def test_gemm_argument_validation():
     assert h.mi355_gemm_bias(1, 1, None, 64, None, 64, None, None, 64, 0, 64, 64, None, None) == 0
 
 
+def test_residual_gemm_and_layernorm_argument_validation():
+    L = _lib()
+    h = L.lib()
+    codes = _status_codes()
+    fake = 1 << 20
+    # residual GEMM: the residual pointer is required, its stride checked like the output's
+    assert h.mi355_gemm_bias_residual(1, 1, fake, 64, fake, 64, None, None, 64, fake, 64, 4, 64, 64,
+                                      None, None) == codes["MI355_E_NULL_POINTER"]
+    assert h.mi355_gemm_bias_residual(1, 1, fake, 64, fake, 64, None, fake, 32, fake, 64, 4, 64, 64,
+                                      None, None) == codes["MI355_E_BAD_SIZE"]
+    assert h.mi355_gemm_bias_residual(1, 2, fake, 64, fake, 64, None, fake, 64, fake, 64, 0, 64, 64,
+                                      None, None) == 0
+    # LayerNorm: sizes, dtype, alignment and the one-wave row limit
+    ln = h.mi355_layernorm
+    assert ln(1, fake, 64, None, None, 1e-5, fake, 64, -1, 64, None) == codes["MI355_E_BAD_SIZE"]
+    assert ln(1, fake, 64, None, None, 1e-5, fake, 64, 4, 0, None) == codes["MI355_E_BAD_SIZE"]
+    assert ln(1, None, 64, None, None, 1e-5, fake, 64, 4, 64, None) == codes["MI355_E_NULL_POINTER"]
+    assert ln(6, fake, 64, None, None, 1e-5, fake, 64, 4, 64, None) == codes["MI355_E_BAD_DTYPE"]
+    assert ln(1, fake, 64, None, None, 1e-5, fake, 64, 4, 60, None) == codes["MI355_E_ALIGNMENT"]
+    assert ln(1, fake, 64, fake + 2, None, 1e-5, fake, 64, 4, 64, None) == codes["MI355_E_ALIGNMENT"]
+    assert ln(1, fake, 32, None, None, 1e-5, fake, 64, 4, 64, None) == codes["MI355_E_BAD_SIZE"]
+    assert ln(1, fake, 64, None, None, -1.0, fake, 64, 4, 64, None) == codes["MI355_E_BAD_SIZE"]
+    assert ln(1, fake, 16384, None, None, 1e-5, fake, 16384, 4, 16384, None) == codes["MI355_E_UNSUPPORTED"]
+    assert ln(0, fake, 8192, None, None, 1e-5, fake, 8192, 4, 8192, None) == codes["MI355_E_UNSUPPORTED"]
+    assert ln(1, fake, 64, None, None, 1e-5, fake, 64, 0, 64, None) == 0
+
+
 def test_attention_argument_validation():
     L = _lib()
     h = L.lib()

@@ -1,0 +1,245 @@
+"""GPU parity of the fused attention half of the transformer block (norm1 -> attention -> residual,
+torch_transformer_benchmark.py:139) and of its two kernels: the row LayerNorm and the residual
+epilogue of the out projection.
+
+Bars:
+* LayerNorm: within one unit in the last place of the output dtype of fp64 LayerNorm of the
+  same (rounded) input, plus 2e-6 times the magnitude of the terms summed (fp32 arithmetic
+  before the one rounding, visible only where gamma * y and beta cancel).
+* residual GEMM: bit-exact against the unfused composition ``dtype(dtype(x @ W^T + b) + r)``
+  computed from the same kernel's plain output (the add is the reference's tensor add of two
+  tensors of the output dtype); masked rows equal the residual exactly.
+* attention half / fused blocks: the benchmark's elementwise predicate (oracle.predicate)
+  against the oracle in fp32 (fp32, fp16) -- for bf16 against the oracle with the bf16 block's
+  rounding points, widened by one bf16 unit in the last place of the attention output, since
+  the reference itself rounds that output to bf16 before the residual add and any difference
+  in the attention output can move that rounding by one step.
+"""
+import os
+import random
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention as OA
+from oracle import model as OM
+from oracle.predicate import compare_outputs
+from tiktok_techjam_2026_track3_amd import workloads as W
+
+pytestmark = pytest.mark.gpu
+
+_rng = random.Random(int.from_bytes(os.urandom(4), "little"))
+RANDOM_SEEDS = tuple(_rng.randrange(2 ** 31) for _ in range(2))
+print(f"random seeds for this run: {RANDOM_SEEDS}", flush=True)
+SEEDS = W.FIXED_SEEDS + RANDOM_SEEDS
+
+MANT = {torch.float16: 10, torch.bfloat16: 7, torch.float32: 23}
+
+
+def _ulp(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    """One unit in the last place of ``dtype`` at the magnitude of ``t`` (normal range)."""
+    e = torch.floor(torch.log2(t.abs().double().clamp_min(torch.finfo(dtype).tiny)))
+    return torch.exp2(e - MANT[dtype])
+
+
+# ------------------------------------------------------------------------------- LayerNorm
+# row lengths up to each dtype's one-wave limit (8192 16-bit or 4096 fp32 elements)
+LN_CASES = [(dt, K) for dt in (torch.float16, torch.bfloat16, torch.float32)
+            for K in (64, 256, 1000, 2048, 4096, 8192) if not (dt == torch.float32 and K > 4096)]
+
+
+@pytest.mark.parametrize("dtype,K", LN_CASES)
+@pytest.mark.parametrize("affine", [False, True])
+def test_layer_norm_within_one_ulp(gpu, dtype, K, affine):
+    from tiktok_techjam_2026_track3_amd import ops
+    g = torch.Generator().manual_seed(K + 3 * affine)
+    M = 301
+    x = (torch.randn(M, K, generator=g) * 2.0 + 0.75).to(dtype)
+    x[3] = 5.0                                   # a constant row: output is the bias
+    w = (torch.randn(K, generator=g) * 0.5 + 1.0).to(dtype) if affine else None
+    b = (torch.randn(K, generator=g) * 0.2).to(dtype) if affine else None
+    print(f"layer_norm dtype={dtype} K={K} affine={affine}", flush=True)
+    out = ops.layer_norm(x.to(gpu), None if w is None else w.to(gpu),
+                         None if b is None else b.to(gpu), 1e-5).cpu()
+    ref = OA.layer_norm(x.double(), None if w is None else w.double(),
+                        None if b is None else b.double(), 1e-5)
+    err = (out.double() - ref).abs()
+    # one ulp of the output dtype, plus the fp32 arithmetic before the single rounding: a few
+    # fp32 ulps of the terms summed (the statistics and (x - mean) at |x| <= ~8, the normalised
+    # value times gamma, and beta), which dominates only where y*gamma and beta cancel
+    terms = 1.0 + (ref - (b.double() if b is not None else 0.0)).abs() + (b.double().abs() if b is not None else 0.0)
+    tol = _ulp(ref, dtype) + 2e-6 * terms
+    bad = err > tol
+    assert not bad.any(), f"{int(bad.sum())} elements beyond 1 ulp, worst {float((err - tol).max())}"
+    want_const = b if b is not None else torch.zeros(K, dtype=dtype)
+    assert torch.equal(out[3], want_const)
+
+
+def test_layer_norm_strided_rows_and_out(gpu):
+    from tiktok_techjam_2026_track3_amd import ops
+    g = torch.Generator().manual_seed(5)
+    big = torch.randn(64, 1536, generator=g).to(torch.float16).to(gpu)
+    x = big[:, 256:1280]                          # row stride 1536, 1024 columns
+    out = torch.full((64, 1280), 7.0, dtype=torch.float16, device=gpu)
+    ops.layer_norm(x, None, None, 1e-5, out=out[:, :1024])
+    assert torch.all(out[:, 1024:] == 7.0)       # nothing written past K
+    ref = ops.layer_norm(x.contiguous(), None, None, 1e-5)
+    assert torch.equal(out[:, :1024], ref)
+
+
+def test_layer_norm_rejects_unsupported_rows(gpu):
+    from tiktok_techjam_2026_track3_amd import ops
+    from tiktok_techjam_2026_track3_amd._lib import KernelError
+    with pytest.raises(KernelError):
+        ops.layer_norm(torch.zeros(4, 8192, device=gpu), None, None)          # fp32 row too long
+    with pytest.raises(KernelError):
+        ops.layer_norm(torch.zeros(4, 100, dtype=torch.float16, device=gpu), None, None)
+
+
+# ---------------------------------------------------------------------- residual epilogue
+@pytest.mark.parametrize("dtype,odt", [(torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16),
+                                       (torch.float32, torch.float32), (torch.float16, torch.bfloat16)])
+@pytest.mark.parametrize("M,N,K", [(300, 520, 256), (1024, 1024, 1024), (64, 100, 128)])
+def test_linear_residual_bit_exact(gpu, dtype, odt, M, N, K):
+    from tiktok_techjam_2026_track3_amd import ops
+    g = torch.Generator().manual_seed(M + N + K)
+    x = torch.randn(M, K, generator=g).to(dtype).to(gpu)
+    wt = (torch.randn(N, K, generator=g) * K ** -0.5).to(dtype).to(gpu)
+    b = torch.randn(N, generator=g).to(gpu)
+    r = (torch.randn(M, N, generator=g) * 2).to(odt).to(gpu)
+    valid = (torch.rand(M, generator=g) > 0.25).to(gpu)
+    print(f"linear residual {dtype}->{odt} M={M} N={N} K={K}", flush=True)
+    plain = ops.linear(x, wt, b, out_dtype=odt)
+    fused = ops.linear(x, wt, b, out_dtype=odt, residual=r)
+    assert torch.equal(fused, (plain.float() + r.float()).to(odt))
+    masked = ops.linear(x, wt, b, out_dtype=odt, residual=r, row_valid=valid)
+    assert torch.equal(masked[valid], fused[valid])
+    assert torch.equal(masked[~valid], r[~valid])
+    inplace = r.clone()
+    ops.linear(x, wt, b, out_dtype=odt, residual=inplace, out=inplace)
+    assert torch.equal(inplace, fused)
+
+
+# ------------------------------------------------------------------------ attention half
+def _half_case(name, seed, gpu, masked):
+    from tiktok_techjam_2026_track3_amd import SelfAttention
+    w = W.CONFIGS[name].scaled(1, 1024 if name != "C1" else 128)
+    params = W.round_params(W.make_params(w), w.dtype)
+    x = W.make_input(w, seed)
+    g = torch.Generator().manual_seed(seed + 1)
+    norm = torch.nn.LayerNorm(w.d_model)
+    with torch.no_grad():
+        norm.weight.copy_(torch.randn(w.d_model, generator=g) * 0.3 + 1.0)
+        norm.bias.copy_(torch.randn(w.d_model, generator=g) * 0.1)
+    norm = norm.to(dtype=w.dtype)
+    wn, bn = norm.weight.detach().float().clone(), norm.bias.detach().float().clone()
+    norm = norm.to(gpu)
+    valid = None
+    if masked:
+        lengths = torch.randint(w.seq // 2, w.seq + 1, (w.batch,), generator=g)
+        valid = torch.arange(w.seq)[None, :] < lengths[:, None]
+    mod = SelfAttention(w.d_model, w.heads)
+    mod.load_state_dict(params)
+    mod = mod.to(device=gpu, dtype=w.dtype)
+    return w, params, x, norm, (wn, bn), valid, mod
+
+
+@pytest.mark.parametrize("masked", [False, True])
+@pytest.mark.parametrize("name", ["C1", "C2", "C3"])
+def test_attention_half_is_the_unfused_composition(gpu, name, masked):
+    """forward_residual == x + forward(layer_norm(x)) bit for bit: the fusion changes no value."""
+    from tiktok_techjam_2026_track3_amd import ops
+    w, params, x, norm, _, valid, mod = _half_case(name, 1234, gpu, masked)
+    xg = x.to(gpu)
+    vg = None if valid is None else valid.to(gpu)
+    with torch.inference_mode():
+        fused = mod.forward_residual(xg, norm, vg, w.causal)
+        h = ops.layer_norm(xg.reshape(-1, w.d_model), norm.weight, norm.bias, norm.eps)
+        comp = xg + mod(h.view_as(xg), vg, w.causal)
+    assert torch.equal(fused, comp)
+    if valid is not None:
+        assert torch.equal(fused[~vg], xg[~vg])
+
+
+@pytest.mark.parametrize("seed", SEEDS)
+@pytest.mark.parametrize("name", ["C1", "C2", "C3"])
+def test_attention_half_matches_oracle(gpu, name, seed):
+    w, params, x, norm, (wn, bn), valid, mod = _half_case(name, seed, gpu, masked=(seed % 2 == 0))
+    pf = {k: v.float() for k, v in params.items()}
+    print(f"attention half {w.name} seed={seed} dtype={w.dtype} causal={w.causal} "
+          f"masked={valid is not None}", flush=True)
+    with torch.inference_mode():
+        out = mod.forward_residual(x.to(gpu), norm, None if valid is None else valid.to(gpu),
+                                   w.causal)
+    assert out.dtype == w.dtype
+    if w.dtype != torch.bfloat16:
+        ref = OA.attention_half(x, wn, bn, pf, w.heads, valid, w.causal, norm.eps)
+        r = compare_outputs(ref, out)
+        print(r.summary(), flush=True)
+        assert r.passed, r.summary()
+        return
+    _assert_bf16_half(x, wn, bn, norm.eps, pf, w.heads, valid, w.causal, out.cpu())
+
+
+def _assert_bf16_half(x, wn, bn, eps, pf, heads, valid, causal, out):
+    """bf16: the predicate against the bf16 block's rounding points, widened by one bf16 ulp of
+    the attention output (rounded before the residual add in the reference)."""
+    ref = OA.attention_half(x, wn, bn, pf, heads, valid, causal, eps, round_to=torch.bfloat16)
+    h = OA.layer_norm(x.float(), wn, bn, eps).to(torch.bfloat16).float()
+    att = OA.self_attention(h, pf, heads, valid, causal)
+    d = (out.float() - ref).abs()
+    ok = torch.isfinite(out.float()) & ((d <= 2e-3 + _ulp(att, torch.bfloat16).float() + _ulp(ref, torch.bfloat16).float())
+                                        | (d <= 2e-2 * ref.abs()))
+    plain = compare_outputs(ref, out)
+    print(f"bf16 half: max |d| {float(d.max()):.3g}, beyond the widened predicate {int((~ok).sum())}; "
+          f"plain predicate: {plain.summary()}", flush=True)
+    assert ok.all()
+
+
+# ------------------------------------------------------------------- plugin fused blocks
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_plugin_fused_blocks_match_oracle_transformer(gpu, dtype, causal):
+    """build(otb, config, fuse_block=True): every block's attention half fused, FFN half torch.
+    Judged block by block against the oracle's block on the same block input (one oracle
+    block in fp32 math with the block dtype's rounding points), then end to end."""
+    from tiktok_techjam_2026_track3_amd import build
+    cfg = OM.TransformerConfig(batch_size=2, seq_len=256, d_model=256, num_heads=4, ffn_dim=512,
+                               num_layers=2, causal=causal)
+    torch.manual_seed(1234)
+    baseline = OM.BaselineTransformer(cfg).eval()
+    cand = build(OM, cfg, fuse_block=True)
+    cand.load_state_dict(baseline.state_dict(), strict=True)
+    cand = cand.to(device=gpu, dtype=dtype).eval()
+    g = torch.Generator().manual_seed(1235)
+    x = torch.randn(2, 256, 256, generator=g).to(dtype)
+    lengths = torch.tensor([256, 173])
+    mask = torch.arange(256)[None, :] < lengths[:, None]
+    x = x.masked_fill(~mask[..., None], 0)
+    print(f"fused plugin dtype={dtype} causal={causal}", flush=True)
+    with torch.inference_mode():
+        h = x.to(gpu)
+        for i, (cl, bl) in enumerate(zip(cand.layers, baseline.layers)):
+            half = cl.attention.forward_residual(h, cl.norm1, mask.to(gpu), causal)
+            pf = {k: v.to(dtype).float() for k, v in bl.attention.state_dict().items()}
+            wn = bl.norm1.weight.detach().to(dtype).float()
+            bn = bl.norm1.bias.detach().to(dtype).float()
+            hin = h.cpu()
+            if dtype == torch.bfloat16:
+                _assert_bf16_half(hin, wn, bn, bl.norm1.eps, pf, cfg.num_heads, mask, causal,
+                                  half.cpu())
+            else:
+                ref = OA.attention_half(hin, wn, bn, pf, cfg.num_heads, mask, causal, bl.norm1.eps)
+                r = compare_outputs(ref, half)
+                print(f"layer {i} attention half:", r.summary(), flush=True)
+                assert r.passed, r.summary()
+            h = cl(h, mask.to(gpu), causal)
+        out = cand(x.to(gpu), mask.to(gpu))
+        assert torch.equal(cand.final_norm(h).masked_fill(~mask.to(gpu)[..., None], 0), out)
+        ref = baseline(x.float(), mask)
+    r = compare_outputs(ref, out)
+    print("end to end vs fp32 oracle transformer (reported for 16-bit):", r.summary(), flush=True)
+    if dtype == torch.float32:
+        assert r.passed, r.summary()
+    assert torch.all(out.cpu()[~mask] == 0)

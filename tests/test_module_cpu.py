@@ -78,6 +78,30 @@ def test_plugin_build_and_swap_keep_state_dict_keys():
     assert all(type(l.attention) is SelfAttention for l in m.layers)
 
 
+def test_plugin_fuse_block_reclasses_blocks_only():
+    from tiktok_techjam_2026_track3_amd.plugin import swap_blocks
+    cfg = OM.TransformerConfig(batch_size=2, seq_len=8, d_model=16, num_heads=4, ffn_dim=16,
+                               num_layers=3, causal=False)
+    torch.manual_seed(9)
+    base = OM.BaselineTransformer(cfg)
+    cand = build(OM, cfg, fuse_block=True)
+    assert all(isinstance(l, OM.BaselineTransformerBlock) for l in cand.layers)
+    assert all(type(l).__name__ == "FusedBaselineTransformerBlock" for l in cand.layers)
+    assert all(type(l.attention) is SelfAttention for l in cand.layers)
+    assert len({type(l) for l in cand.layers}) == 1          # one derived class, reused
+    res = cand.load_state_dict(base.state_dict(), strict=True)
+    assert not res.missing_keys and not res.unexpected_keys
+    assert swap_blocks(cand) == 3                             # idempotent: same classes again
+    assert len({type(l) for l in cand.layers}) == 1
+    with pytest.raises(ValueError):
+        build(OM, cfg, int8=True, fuse_block=True)
+    # no CPU route: the fused block's forward raises on CPU tensors
+    with pytest.raises(Exception):
+        cand(torch.randn(2, 8, 16), torch.ones(2, 8, dtype=torch.bool))
+    with pytest.raises(NotImplementedError):
+        Int8SelfAttention(16, 4).forward_residual(torch.randn(1, 8, 16), torch.nn.LayerNorm(16))
+
+
 def test_workload_accounting():
     c2 = W.CONFIGS["C2"]
     f = c2.flops()

@@ -116,6 +116,90 @@ def test_all_keys_masked_row_is_nan_and_zeroed_by_row_mask():
     assert torch.isfinite(out[0]).all()
 
 
+# -------------------------------------------------------------------- LayerNorm, block half
+@pytest.mark.parametrize("affine", [False, True])
+def test_layer_norm_matches_bruteforce_and_torch(affine):
+    g = torch.Generator().manual_seed(21)
+    x = torch.randn(5, 3, 48, generator=g) * 2.5 + 0.7
+    w = torch.randn(48, generator=g) if affine else None
+    b = torch.randn(48, generator=g) if affine else None
+    got = OA.layer_norm(x, w, b, 1e-5)
+    want = OA.layer_norm_bruteforce(x.numpy(), None if w is None else w.numpy(),
+                                    None if b is None else b.numpy(), 1e-5)
+    np.testing.assert_allclose(got.numpy(), want, rtol=2e-6, atol=2e-6)
+    lib = torch.nn.functional.layer_norm(x, (48,), w, b, 1e-5)
+    np.testing.assert_allclose(lib.numpy(), want, rtol=2e-6, atol=2e-6)
+
+
+def test_layer_norm_closed_forms():
+    w = torch.tensor([2.0, -3.0, 0.5, 1.0])
+    b = torch.tensor([0.25, -1.0, 4.0, 0.0])
+    const = torch.full((2, 4), 7.5)
+    # a constant row has x - mean = 0 exactly: the output is the bias
+    assert torch.equal(OA.layer_norm(const, w, b), b.expand(2, 4))
+    # [a, -a] with eps = 0 has mean 0, biased variance a^2: normalised to [1, -1]
+    two = torch.tensor([[3.0, -3.0], [-0.5, 0.5]])
+    assert torch.allclose(OA.layer_norm(two, None, None, 0.0), torch.tensor([[1.0, -1.0], [-1.0, 1.0]]))
+    # eps = 0: invariant under x -> c * x + s for c > 0, sign-flipped for c < 0
+    x = torch.randn(3, 32, generator=torch.Generator().manual_seed(4), dtype=torch.float64)
+    y = OA.layer_norm(x, None, None, 0.0)
+    assert torch.allclose(OA.layer_norm(4.0 * x - 9.0, None, None, 0.0), y, atol=1e-12)
+    assert torch.allclose(OA.layer_norm(-0.25 * x + 3.0, None, None, 0.0), -y, atol=1e-12)
+    # eps inside the square root: [e, -e] rows shrink to e / sqrt(e^2 + eps)
+    tiny = torch.tensor([[1e-3, -1e-3]], dtype=torch.float64)
+    assert torch.allclose(OA.layer_norm(tiny, None, None, 1e-5),
+                          torch.tensor([[1.0, -1.0]], dtype=torch.float64) * 1e-3 / (1e-6 + 1e-5) ** 0.5)
+
+
+@pytest.mark.parametrize("mistake", ["unbiased", "eps_outside", "no_centering"])
+def test_planted_layer_norm_mistakes_fail_the_pin(mistake):
+    x = torch.randn(4, 16, generator=torch.Generator().manual_seed(8)) + 1.0
+    want = OA.layer_norm_bruteforce(x.numpy(), None, None, 1e-2)
+    mean = x.mean(-1, keepdim=True)
+    var = x.var(-1, keepdim=True, unbiased=(mistake == "unbiased"))
+    if mistake == "eps_outside":
+        bad = (x - mean) / (torch.sqrt(var) + 1e-2)
+    elif mistake == "no_centering":
+        bad = x / torch.sqrt(var + 1e-2)
+    else:
+        bad = (x - mean) / torch.sqrt(var + 1e-2)
+    assert not np.allclose(bad.numpy(), want, atol=1e-4)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("masked", [False, True])
+def test_attention_half_matches_bruteforce(causal, masked):
+    B, S, d, H = 2, 7, 16, 2
+    g = torch.Generator().manual_seed(31)
+    x = torch.randn(B, S, d, generator=g) * 1.5 + 0.3
+    w, b = torch.randn(d, generator=g), torch.randn(d, generator=g)
+    p = _params(d, seed=32)
+    valid = torch.rand(B, S, generator=g) > 0.3 if masked else None
+    if valid is not None:
+        valid[:, 0] = True
+    got = OA.attention_half(x, w, b, p, H, valid, causal)
+    h = OA.layer_norm_bruteforce(x.numpy(), w.numpy(), b.numpy(), 1e-5)
+    att = OA.self_attention_bruteforce(h, {k: v.numpy() for k, v in p.items()}, H, causal,
+                                       None if valid is None else valid.numpy())
+    np.testing.assert_allclose(got.numpy(), x.numpy() + att, rtol=2e-5, atol=2e-5)
+    if valid is not None:
+        # rows masked out of the attention output keep the residual input exactly
+        assert torch.equal(got[~valid], x[~valid])
+
+
+def test_attention_half_rounding_points():
+    """round_to rounds the norm output, the attention output and the sum: with bf16 the
+    result is representable in bf16 and differs from the fp32 half by rounding only."""
+    g = torch.Generator().manual_seed(33)
+    x = (torch.randn(1, 9, 16, generator=g)).to(torch.bfloat16)
+    w, b = torch.randn(16, generator=g), torch.randn(16, generator=g)
+    p = _params(16, seed=34)
+    r = OA.attention_half(x, w, b, p, 2, round_to=torch.bfloat16)
+    assert torch.equal(r, r.to(torch.bfloat16).float())
+    f = OA.attention_half(x, w, b, p, 2)
+    assert (r - f).abs().max() < 0.1 and not torch.equal(r, f)
+
+
 def test_qkv_projection_equals_separate_projections():
     p = _params(16)
     x = torch.randn(2, 3, 16)

@@ -2,18 +2,19 @@
 
 Public API:
   SelfAttention, Int8SelfAttention      drop-in modules for BaselineSelfAttention
-  build, swap_attention,
-  make_user_optimized_transformer       the reference's plugin insertion points
+  build, swap_attention, swap_blocks,
+  make_user_optimized_transformer       the reference's plugin insertion points (swap_blocks: the
+                                        attention half of each block fused)
   ops                                   torch wrappers of the C-ABI kernels
   workloads                             the measured configurations and seeded inputs
 """
 from .attention import Int8SelfAttention, SelfAttention
-from .plugin import build, make_user_optimized_transformer, swap_attention
+from .plugin import build, make_user_optimized_transformer, swap_attention, swap_blocks
 from . import ops, workloads
 
 BaselineSelfAttention = SelfAttention  # the reference's class name
 
 __all__ = [
     "SelfAttention", "Int8SelfAttention", "BaselineSelfAttention", "build", "swap_attention",
-    "make_user_optimized_transformer", "ops", "workloads",
+    "make_user_optimized_transformer", "swap_blocks", "ops", "workloads",
 ]

@@ -35,6 +35,11 @@ _SIGNATURES = {
          C.c_float, C.c_int, _P, _I64, _P],
     ),
     "mi355_quant_rows_i8": (C.c_int, [C.c_int, _P, _I64, _P, _P, _I64, _I64, C.c_int, _P]),
+    "mi355_layernorm": (C.c_int, [C.c_int, _P, _I64, _P, _P, C.c_float, _P, _I64, _I64, _I64, _P]),
+    "mi355_gemm_bias_residual": (
+        C.c_int,
+        [C.c_int, C.c_int, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P],
+    ),
     "mi355_gemm_i8": (
         C.c_int,
         [_P, _P, _P, _P, _P, C.c_int, _P, _I64, _P, _I64, _I64, _I64, _P, _P],

@@ -174,6 +174,46 @@ class SelfAttention(nn.Module):
             keep.update(qkv=qkv, ctx=ctx)
         return out.view(B, S, d)
 
+    def forward_residual(self, x: torch.Tensor, norm: nn.LayerNorm,
+                         valid_token_mask: Optional[torch.Tensor] = None, causal: bool = False,
+                         marks: Optional[Callable[[str], None]] = None) -> torch.Tensor:
+        """``x + self(norm(x), valid_token_mask, causal)``: the attention half of
+        BaselineTransformerBlock.forward (torch_transformer_benchmark.py:139).
+
+        The LayerNorm runs as its own row kernel (fp32 statistics, rounded to x's dtype as
+        nn.LayerNorm's output is) and the residual add is fused into the out projection's
+        epilogue, where the projection is rounded to x's dtype before the add, as in the
+        reference; rows masked out keep x. ``marks`` as for ``run`` with an extra "norm" stage.
+        """
+        mark = marks or (lambda _stage: None)
+        B, S = self._check_input(x)
+        d = self.d_model
+        if tuple(norm.normalized_shape) != (d,):
+            raise ValueError(f"norm must normalise the last dimension ({d})")
+        w_n, b_n = norm.weight, norm.bias
+        for t in (w_n, b_n):
+            if t is not None and (t.dtype != x.dtype or t.device != x.device):
+                raise ValueError("norm parameters must be on x's device in x's dtype")
+        key_valid, row_valid = self._resolve_mask(valid_token_mask, B, S, x.device)
+        w_qkv, b_qkv, w_o, b_o = self._packed_weights(x.dtype, x.device)
+        core = self.core_dtype(x.dtype)
+        x2 = x.reshape(B * S, d)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        mark("norm")
+        h = ops.layer_norm(x2, w_n.detach() if w_n is not None else None,
+                           b_n.detach() if b_n is not None else None, norm.eps)
+        mark("qkv")
+        qkv = ops.linear(h, w_qkv, b_qkv, out_dtype=core)
+        q, k, v = self._qkv_views(qkv, B, S)
+        mark("attn")
+        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid)
+        mark("out")
+        out = ops.linear(ctx.view(B * S, d), w_o, b_o, row_valid=row_valid, out_dtype=x.dtype,
+                         residual=x2)
+        mark("end")
+        return out.view(B, S, d)
+
 
 class Int8SelfAttention(SelfAttention):
     """W8A8 variant: int8 projections with exact int32 accumulation, fp16 SDPA.
@@ -225,3 +265,7 @@ class Int8SelfAttention(SelfAttention):
         if keep is not None:
             keep.update(qkv=qkv, ctx=ctx, x_i8=xq, x_scale=sx, ctx_i8=cq, ctx_scale=sc)
         return out.view(B, S, d)
+
+    def forward_residual(self, *args, **kwargs):
+        raise NotImplementedError("the fused norm + residual path is built for the 16-bit / fp32 "
+                                  "block; the int8 block's attention runs through run()")

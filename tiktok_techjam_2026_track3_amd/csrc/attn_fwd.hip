@@ -598,8 +598,11 @@ __global__ __launch_bounds__(64) void attn_fwd_f32(AttnArgs p) {
 #ifndef MI355_ATTN_WPE128
 #define MI355_ATTN_WPE128 1
 #endif
-#ifndef MI355_ATTN_PRIO
-#define MI355_ATTN_PRIO 0
+#ifndef MI355_ATTN_PRIO64
+#define MI355_ATTN_PRIO64 0
+#endif
+#ifndef MI355_ATTN_PRIO128
+#define MI355_ATTN_PRIO128 0
 #endif
 // score look-ahead (software pipeline) for unmasked head_dim 64; measured no faster on gfx950
 // than the double-buffered loop, so off by default
@@ -611,8 +614,8 @@ template <typename T, int HD, int NW, int QG, bool CAUSAL, bool KMASK>
 void launch_one(const AttnArgs& a, dim3 grid, dim3 block, hipStream_t s) {
   constexpr int KT = HD == 64 ? MI355_ATTN_KT64 : MI355_ATTN_KT128;
   constexpr int WPE = HD == 64 ? MI355_ATTN_WPE64 : MI355_ATTN_WPE128;
-  constexpr bool PRIO = MI355_ATTN_PRIO != 0;
-  constexpr bool PIPE = HD == 64 && !KMASK && MI355_ATTN_PIPE64 != 0;
+  constexpr bool PRIO = (HD == 64 ? MI355_ATTN_PRIO64 : MI355_ATTN_PRIO128) != 0;
+  constexpr bool PIPE = HD == 64 && (!KMASK || MI355_ATTN_PIPE64 > 1) && MI355_ATTN_PIPE64 != 0;
   hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, KT, WPE, PRIO, PIPE, CAUSAL, KMASK>), grid, block, 0, s, a);
 }
 

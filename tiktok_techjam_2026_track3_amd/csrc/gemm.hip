@@ -25,7 +25,8 @@ struct GemmArgs {
   const float* s_a;  // int8 only
   const float* s_w;  // int8 only
   const uint8_t* row_valid;
-  int64_t lda, ldw, ldc;
+  const void* R;  // residual [M, N] of the output dtype, nullable: C = R + round(A W^T + b)
+  int64_t lda, ldw, ldc, ldr;
   int64_t M, N, K;
   int out_dtype;
 };
@@ -335,8 +336,13 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
         } else {
           if (p.C && in_m) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e)
-              if (n0 + n_loc + e < p.N) store_out<TO>(p.C, m * p.ldc + n0 + n_loc + e, v[e]);
+            for (int e = 0; e < 4; ++e) {
+              const int64_t n = n0 + n_loc + e;
+              if (n >= p.N) continue;
+              float y = to_f32(from_f32<TO>(v[e]));  // the projection output, rounded once
+              if (p.R) y = y + to_f32(static_cast<const TO*>(p.R)[m * p.ldr + n]);
+              store_out<TO>(p.C, m * p.ldc + n, y);
+            }
           }
         }
       }
@@ -348,18 +354,65 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
       // coalesced copy of the staged tile: 16-byte chunks, rows of BN outputs
       constexpr int CPR = BN * static_cast<int>(sizeof(TO)) / 16;  // chunks per row
       constexpr int EPC_OUT = 16 / static_cast<int>(sizeof(TO));
-      const bool vec_ok = (p.ldc % EPC_OUT) == 0 && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0);
+      const bool vec_ok = (p.ldc % EPC_OUT) == 0 && ((reinterpret_cast<uintptr_t>(p.C) & 15u) == 0) &&
+                          (!p.R || ((p.ldr % EPC_OUT) == 0 && (reinterpret_cast<uintptr_t>(p.R) & 15u) == 0));
+      constexpr int PER = BM * CPR / NT;  // chunks per thread
+      static_assert((BM * CPR) % NT == 0, "epilogue chunks");
+      if (p.R && vec_ok) {
+        // residual: every residual chunk of this thread is requested before the first is used,
+        // so the loads' latency is paid once rather than once per chunk. Each chunk is read
+        // before the same thread writes it, so R may be C.
+        const TO* Rb = static_cast<const TO*>(p.R);
+        u32x4 rc[PER];
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int idx = tid + i * NT, r = idx / CPR, c = idx % CPR;
+          const int64_t m = m0 + r, n = n0 + static_cast<int64_t>(c) * EPC_OUT;
+          rc[i] = u32x4{0u, 0u, 0u, 0u};
+          if (m < p.M && n + EPC_OUT <= p.N) rc[i] = *reinterpret_cast<const u32x4*>(Rb + m * p.ldr + n);
+        }
+#pragma unroll
+        for (int i = 0; i < PER; ++i) {
+          const int idx = tid + i * NT, r = idx / CPR, c = idx % CPR;
+          const int64_t m = m0 + r, n = n0 + static_cast<int64_t>(c) * EPC_OUT;
+          if (m >= p.M || n >= p.N) continue;
+          u32x4 chunk = *reinterpret_cast<const u32x4*>(cl + r * C_PITCH + c * 16);
+          TO* dst = static_cast<TO*>(p.C) + m * p.ldc + n;
+          TO* cv = reinterpret_cast<TO*>(&chunk);
+          if (n + EPC_OUT <= p.N) {
+            const TO* rv = reinterpret_cast<const TO*>(&rc[i]);
+#pragma unroll
+            for (int e = 0; e < EPC_OUT; ++e) cv[e] = from_f32<TO>(to_f32(cv[e]) + to_f32(rv[e]));
+            *reinterpret_cast<u32x4*>(dst) = chunk;
+          } else {
+            const TO* res = Rb + m * p.ldr + n;
+            for (int e = 0; e < EPC_OUT && n + e < p.N; ++e)
+              dst[e] = from_f32<TO>(to_f32(cv[e]) + to_f32(res[e]));
+          }
+        }
+      } else
       for (int idx = tid; idx < BM * CPR; idx += NT) {
         const int r = idx / CPR, c = idx % CPR;
         const int64_t m = m0 + r, n = n0 + static_cast<int64_t>(c) * EPC_OUT;
         if (m >= p.M || n >= p.N) continue;
-        const u32x4 chunk = *reinterpret_cast<const u32x4*>(cl + r * C_PITCH + c * 16);
+        u32x4 chunk = *reinterpret_cast<const u32x4*>(cl + r * C_PITCH + c * 16);
         TO* dst = static_cast<TO*>(p.C) + m * p.ldc + n;
+        const TO* res = p.R ? static_cast<const TO*>(p.R) + m * p.ldr + n : nullptr;
         if (vec_ok && n + EPC_OUT <= p.N) {
+          if (res) {
+            // residual add on the rounded projection output (the reference adds two tensors of
+            // the output dtype); read before the write, so R may be C itself
+            const u32x4 rc = *reinterpret_cast<const u32x4*>(res);
+            TO* cv = reinterpret_cast<TO*>(&chunk);
+            const TO* rv = reinterpret_cast<const TO*>(&rc);
+#pragma unroll
+            for (int e = 0; e < EPC_OUT; ++e) cv[e] = from_f32<TO>(to_f32(cv[e]) + to_f32(rv[e]));
+          }
           *reinterpret_cast<u32x4*>(dst) = chunk;
         } else {
           const TO* src = reinterpret_cast<const TO*>(&chunk);
-          for (int e = 0; e < EPC_OUT && n + e < p.N; ++e) dst[e] = src[e];
+          for (int e = 0; e < EPC_OUT && n + e < p.N; ++e)
+            dst[e] = res ? from_f32<TO>(to_f32(src[e]) + to_f32(res[e])) : src[e];
         }
       }
     }
@@ -408,10 +461,10 @@ int launch_by_out(const GemmArgs& a, hipStream_t s) {
   }
 }
 
-extern "C" int mi355_gemm_bias(int in_dtype, int out_dtype, const void* A, int64_t lda,
-                               const void* W, int64_t ldw, const float* bias, void* C, int64_t ldc,
-                               int64_t M, int64_t N, int64_t K, const uint8_t* row_valid,
-                               void* stream) {
+namespace {
+int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, const void* W, int64_t ldw,
+                   const float* bias, const void* R, int64_t ldr, void* C, int64_t ldc, int64_t M,
+                   int64_t N, int64_t K, const uint8_t* row_valid, void* stream) {
   if (M < 0 || N < 0 || K < 0) return MI355_E_BAD_SIZE;
   if (M == 0 || N == 0) return MI355_OK;
   if (!A || !W || !C) return MI355_E_NULL_POINTER;
@@ -422,16 +475,18 @@ extern "C" int mi355_gemm_bias(int in_dtype, int out_dtype, const void* A, int64
   const int64_t epc = in_dtype == MI355_F32 ? 4 : 8;
   if (K % epc || lda % epc || ldw % epc || !aligned16(A) || !aligned16(W))
     return MI355_E_ALIGNMENT;
-  if (lda < K || ldw < K || ldc < N) return MI355_E_BAD_SIZE;
+  if (lda < K || ldw < K || ldc < N || (R && ldr < N)) return MI355_E_BAD_SIZE;
   GemmArgs a{};
   a.A = A;
   a.W = W;
   a.bias = bias;
   a.C = C;
+  a.R = R;
   a.row_valid = row_valid;
   a.lda = lda;
   a.ldw = ldw;
   a.ldc = ldc;
+  a.ldr = ldr;
   a.M = M;
   a.N = N;
   a.K = K;
@@ -442,6 +497,24 @@ extern "C" int mi355_gemm_bias(int in_dtype, int out_dtype, const void* A, int64
     case MI355_BF16: return launch_by_out<__bf16, 256, 256, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
     default: return launch_gemm<float, float, 128, 128, 2, 2, false>(a, s);
   }
+}
+}  // namespace
+
+extern "C" int mi355_gemm_bias(int in_dtype, int out_dtype, const void* A, int64_t lda,
+                               const void* W, int64_t ldw, const float* bias, void* C, int64_t ldc,
+                               int64_t M, int64_t N, int64_t K, const uint8_t* row_valid,
+                               void* stream) {
+  return gemm_bias_impl(in_dtype, out_dtype, A, lda, W, ldw, bias, nullptr, 0, C, ldc, M, N, K,
+                        row_valid, stream);
+}
+
+extern "C" int mi355_gemm_bias_residual(int in_dtype, int out_dtype, const void* A, int64_t lda,
+                                        const void* W, int64_t ldw, const float* bias, const void* R,
+                                        int64_t ldr, void* C, int64_t ldc, int64_t M, int64_t N,
+                                        int64_t K, const uint8_t* row_valid, void* stream) {
+  if (M > 0 && N > 0 && !R) return MI355_E_NULL_POINTER;
+  return gemm_bias_impl(in_dtype, out_dtype, A, lda, W, ldw, bias, R, ldr, C, ldc, M, N, K,
+                        row_valid, stream);
 }
 
 extern "C" int mi355_gemm_i8(const int8_t* A, const int8_t* W, const float* s_a, const float* s_w,

@@ -1,0 +1,126 @@
+// Row LayerNorm (nn.LayerNorm over the last dimension) for gfx950:
+//   y = (x - mean) * rstd * gamma + beta,  rstd = 1 / sqrt(var + eps),  var biased (divide by K)
+// Statistics and the affine map are fp32; y is rounded once to the input dtype. One wave per row,
+// the row held in registers as 16-byte vectors (up to 64 * NV vectors), two-pass mean / variance.
+// HBM-bound: reads the row once and writes it once.
+#include "common.h"
+
+namespace {
+
+MI355_DEVINL float wave_sum(float v) {
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  return v;
+}
+
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, int64_t ldx,
+                                                      const T* __restrict__ gamma,
+                                                      const T* __restrict__ beta, float eps,
+                                                      T* __restrict__ Y, int64_t ldy, int64_t M,
+                                                      int K) {
+  constexpr int EPV = 16 / static_cast<int>(sizeof(T));  // elements per 16-byte vector
+  typedef T tv __attribute__((ext_vector_type(EPV)));
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;  // whole wave leaves together
+  const int nvec = K / EPV;
+  const T* xr = X + row * ldx;
+
+  float xs[NV][EPV];
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int vi = lane + 64 * j;
+    tv v = {};
+    if (vi < nvec) v = *reinterpret_cast<const tv*>(xr + static_cast<int64_t>(vi) * EPV);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      xs[j][e] = to_f32(v[e]);
+      sum += xs[j][e];
+    }
+  }
+  const float mean = wave_sum(sum) / static_cast<float>(K);
+  float sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    if (lane + 64 * j < nvec) {
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) {
+        const float d = xs[j][e] - mean;
+        sq += d * d;
+      }
+    }
+  }
+  const float var = wave_sum(sq) / static_cast<float>(K);
+  const float rstd = 1.0f / sqrtf(var + eps);
+
+  T* yr = Y + row * ldy;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int vi = lane + 64 * j;
+    if (vi >= nvec) continue;
+    tv gv, bv;
+    if (gamma) gv = *reinterpret_cast<const tv*>(gamma + static_cast<int64_t>(vi) * EPV);
+    if (beta) bv = *reinterpret_cast<const tv*>(beta + static_cast<int64_t>(vi) * EPV);
+    tv out;
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      float y = (xs[j][e] - mean) * rstd;
+      if (gamma) y = y * to_f32(gv[e]);
+      if (beta) y = y + to_f32(bv[e]);
+      out[e] = from_f32<T>(y);
+    }
+    *reinterpret_cast<tv*>(yr + static_cast<int64_t>(vi) * EPV) = out;
+  }
+}
+
+template <typename T>
+int launch_ln(const void* X, int64_t ldx, const void* gamma, const void* beta, float eps, void* Y,
+              int64_t ldy, int64_t M, int64_t K, hipStream_t s) {
+  constexpr int EPV = 16 / static_cast<int>(sizeof(T));
+  const int64_t nvec = K / EPV;
+  const int64_t blocks = (M + 3) / 4;
+  if (blocks > 0x7fffffffLL) return MI355_E_BAD_SIZE;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  const T* x = static_cast<const T*>(X);
+  const T* g = static_cast<const T*>(gamma);
+  const T* b = static_cast<const T*>(beta);
+  T* y = static_cast<T*>(Y);
+  const int k = static_cast<int>(K);
+  if (nvec <= 64)
+    hipLaunchKernelGGL((layernorm_rows<T, 1>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k);
+  else if (nvec <= 128)
+    hipLaunchKernelGGL((layernorm_rows<T, 2>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k);
+  else if (nvec <= 256)
+    hipLaunchKernelGGL((layernorm_rows<T, 4>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k);
+  else if (nvec <= 512)
+    hipLaunchKernelGGL((layernorm_rows<T, 8>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k);
+  else
+    hipLaunchKernelGGL((layernorm_rows<T, 16>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k);
+  return static_cast<int>(hipGetLastError());
+}
+
+}  // namespace
+
+extern "C" int mi355_layernorm(int dtype, const void* X, int64_t ldx, const void* gamma,
+                               const void* beta, float eps, void* Y, int64_t ldy, int64_t M,
+                               int64_t K, void* stream) {
+  if (M < 0 || K <= 0) return MI355_E_BAD_SIZE;
+  if (M == 0) return MI355_OK;
+  if (!X || !Y) return MI355_E_NULL_POINTER;
+  if (dtype != MI355_F32 && dtype != MI355_F16 && dtype != MI355_BF16) return MI355_E_BAD_DTYPE;
+  if (!(eps >= 0.f)) return MI355_E_BAD_SIZE;
+  const int64_t epv = dtype == MI355_F32 ? 4 : 8;
+  if (K % epv || ldx % epv || ldy % epv || !aligned16(X) || !aligned16(Y) ||
+      (gamma && !aligned16(gamma)) || (beta && !aligned16(beta)))
+    return MI355_E_ALIGNMENT;
+  if (ldx < K || ldy < K) return MI355_E_BAD_SIZE;
+  if (K / epv > 64 * 16) return MI355_E_UNSUPPORTED;  // row must fit the registers of one wave
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  switch (dtype) {
+    case MI355_F16: return launch_ln<_Float16>(X, ldx, gamma, beta, eps, Y, ldy, M, K, s);
+    case MI355_BF16: return launch_ln<__bf16>(X, ldx, gamma, beta, eps, Y, ldy, M, K, s);
+    default: return launch_ln<float>(X, ldx, gamma, beta, eps, Y, ldy, M, K, s);
+  }
+}

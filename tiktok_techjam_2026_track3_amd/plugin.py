@@ -13,6 +13,7 @@
 from __future__ import annotations
 
 import torch.nn as nn
+import torch.nn.functional as F
 
 from .attention import Int8SelfAttention, SelfAttention
 
@@ -35,21 +36,69 @@ def swap_attention(model: nn.Module, int8: bool = False) -> int:
     return swapped
 
 
-def build(otb, config, int8: bool = False) -> nn.Module:
-    """Plugin contract of the reference harness: a model whose attention runs on gfx950."""
+_BLOCK_ATTRS = ("norm1", "attention", "norm2", "ffn_in", "ffn_out")
+_FUSED_CLASSES: dict = {}
+
+
+def _fused_block_forward(self, x, valid_token_mask, causal):
+    """BaselineTransformerBlock.forward (torch_transformer_benchmark.py:134-146) with its attention
+    half -- ``x + attention(norm1(x))`` -- on the gfx950 kernels (LayerNorm kernel, fused residual
+    epilogue); the FFN half is the reference's own code."""
+    x = self.attention.forward_residual(x, self.norm1, valid_token_mask, causal)
+    x = x + self.ffn_out(F.gelu(self.ffn_in(self.norm2(x)), approximate="none"))
+    if valid_token_mask is not None:
+        x = x.masked_fill(~valid_token_mask[..., None], 0)
+    return x
+
+
+def _fused_class(cls):
+    if cls not in _FUSED_CLASSES:
+        _FUSED_CLASSES[cls] = type("Fused" + cls.__name__, (cls,), {"forward": _fused_block_forward})
+    return _FUSED_CLASSES[cls]
+
+
+def swap_blocks(model: nn.Module) -> int:
+    """Re-class every transformer block of ``model`` (modules with norm1 / attention / norm2 /
+    ffn_in / ffn_out) so its attention half runs fused, and its attention on gfx950; returns how
+    many blocks were swapped. Parameters and state-dict keys are untouched."""
+    swapped = 0
+    for mod in list(model.modules()):
+        if all(hasattr(mod, a) for a in _BLOCK_ATTRS) and _is_attention(mod.attention):
+            if not isinstance(mod.attention, SelfAttention) or isinstance(mod.attention, Int8SelfAttention):
+                mod.attention.__class__ = SelfAttention
+                mod.attention.invalidate_caches()
+            if type(mod) not in _FUSED_CLASSES.values():
+                mod.__class__ = _fused_class(type(mod))
+            swapped += 1
+    return swapped
+
+
+def build(otb, config, int8: bool = False, fuse_block: bool = False) -> nn.Module:
+    """Plugin contract of the reference harness: a model whose attention runs on gfx950.
+
+    ``fuse_block`` also runs each block's attention half (norm1, attention, residual add) as
+    LayerNorm kernel + attention + out projection with the residual fused into its epilogue."""
+    if int8 and fuse_block:
+        raise ValueError("the fused norm + residual path is built for the 16-bit / fp32 block")
     base = getattr(otb, "UserOptimizedTransformer", None) or otb.BaselineTransformer
     model = base(config)
     if swap_attention(model, int8=int8) == 0:
         raise RuntimeError("no attention module found to replace")
+    if fuse_block and swap_blocks(model) == 0:
+        raise RuntimeError("no transformer block found to fuse")
     return model
 
 
-def make_user_optimized_transformer(otb, int8: bool = False):
+def make_user_optimized_transformer(otb, int8: bool = False, fuse_block: bool = False):
     """A ``UserOptimizedTransformer`` class for the official script module ``otb``."""
+    if int8 and fuse_block:
+        raise ValueError("the fused norm + residual path is built for the 16-bit / fp32 block")
 
     class UserOptimizedTransformer(otb.BaselineTransformer):
         def __init__(self, config):
             super().__init__(config)
             swap_attention(self, int8=int8)
+            if fuse_block:
+                swap_blocks(self)
 
     return UserOptimizedTransformer
