@@ -106,6 +106,22 @@ MI355_DEVINL float pair_max(float v) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
 }
+// LDS DMA (global -> LDS, lane i's 16 bytes at lds_addr + 16 i; 1-byte form: lane i's byte
+// zero-extended at lds_addr + 4 i), issued through inline assembly so that the compiler does not
+// treat it as a pending LDS write: with the builtin it makes every later LDS wait a full
+// lgkmcnt(0) while the load is in flight, and adds vmcnt waits before transpose reads. Callers
+// order the data themselves (s_waitcnt vmcnt + a work-group barrier before the destination is
+// read) and never read a destination while its load is in flight. lds_addr must be wave-uniform.
+MI355_DEVINL void dma_lds16(const void* gptr, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr),
+               "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
+MI355_DEVINL void dma_lds1(const void* gptr, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_ubyte %0, off" ::"v"(gptr),
+               "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
 MI355_DEVINL float pair_sum(float v) {
   auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
@@ -117,6 +133,11 @@ MI355_DEVINL int elem_size(int dtype) { return dtype == MI355_F32 ? 4 : 2; }
 // base + soffset + voffset, landing at LDS lds_base + 16 * lane. The resource covers `bytes` bytes
 // from `base` (the range check includes soffset); dwords past it read as 0. The resource is built in these device functions so its type
 // never appears in host-compiled code.
+template <typename P>
+MI355_DEVINL uint32_t lds_addr_of(P* p) {
+  return static_cast<uint32_t>(reinterpret_cast<uintptr_t>(
+      (__attribute__((address_space(3))) const void*)(p)));
+}
 MI355_DEVINL __amdgpu_buffer_rsrc_t raw_rsrc(const void* base, uint32_t bytes) {
   return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), 0, static_cast<int>(bytes),
                                            0x00020000 /* raw buffer, 32-bit data format */);
