@@ -50,6 +50,10 @@ def parse_args():
                          "(torch_transformer_benchmark.py:139): LayerNorm kernel, QKV projection, "
                          "attention, out projection with the residual add in its epilogue "
                          "(16-bit / fp32 configurations)")
+    ap.add_argument("--graph", action="store_true",
+                    help="time replays of one step captured in a HIP graph (torch.cuda.CUDAGraph): "
+                         "no per-kernel host launch cost; the per-stage breakdown still comes from "
+                         "the eager loop")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain copy kernel (y = -x, fp16) over BYTES bytes, three times; "
                          "profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE it calibrates the "
@@ -163,7 +167,7 @@ def cpu_baseline(w, budget_s: float) -> dict:
 
 # ------------------------------------------------------------------------------ gpu measure
 def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
-            half: bool = False) -> dict:
+            half: bool = False, graph: bool = False) -> dict:
     import torch
     from tiktok_techjam_2026_track3_amd import Int8SelfAttention, SelfAttention
     from tiktok_techjam_2026_track3_amd import workloads as W
@@ -231,6 +235,28 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
             torch.cuda.synchronize()
             unfused_ms = u0.elapsed_time(u1) / steps
     ms_step = start.elapsed_time(end) / steps
+    eager_ms = ms_step
+    if graph:
+        # one step captured once (after a side-stream warm-up, as capture requires), then replayed
+        with torch.inference_mode():
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                step()
+            torch.cuda.current_stream().wait_stream(side)
+            g = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(g):
+                step()
+            for _ in range(max(3, warmup)):
+                g.replay()
+            torch.cuda.synchronize()
+            g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            g0.record()
+            for _ in range(steps):
+                g.replay()
+            g1.record()
+            torch.cuda.synchronize()
+        ms_step = g0.elapsed_time(g1) / steps
     fl = w.flops()
     by = dict(w.bytes())
     if half:
@@ -284,6 +310,8 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
                      "algorithmic_bytes": by[dom], "dtype": kdt},
         "stages": stage_report,
         "wall_s": round(wall, 3),
+        "launch": "graph replay" if graph else "eager",
+        **({"eager_ms_per_step": round(eager_ms, 5)} if graph else {}),
         **({"unfused_half_ms_per_step": round(unfused_ms, 5)} if unfused_ms is not None else {}),
         "warmup_steps_run": n_warm,
         "warmup_s": round(warm_s, 3),
@@ -313,7 +341,8 @@ def main() -> int:
             log(f"unknown config {name}")
             return 2
         log(f"[bench] {name}: warmup {args.warmup}, steps {args.steps}")
-        res = measure(name, args.steps, args.warmup, args.min_warmup_s, args.attention_half)
+        res = measure(name, args.steps, args.warmup, args.min_warmup_s, args.attention_half,
+                      args.graph)
         log(f"[bench] {name}: {res['ms_per_step']} ms/step, {res['value']} {res['unit']}")
         if not args.no_cpu_baseline:
             log(f"[bench] {name}: cpu baseline (budget {args.cpu_budget}s)")

@@ -199,3 +199,36 @@ def test_plugin_build_matches_oracle_transformer(gpu):
     r = compare_outputs(ref, out)
     print(r.summary(), flush=True)
     assert r.passed, r.summary()
+
+
+@pytest.mark.parametrize("name,masked,half", [("C1", True, False), ("C2", False, False),
+                                              ("C3", True, True)])
+def test_graphed_forward_replays_match_eager(gpu, name, masked, half):
+    """GraphedForward (whole-forward capture): every replay equals the eager forward bit for bit,
+    with unrelated eager work and synchronisations between replays; a parameter update after
+    capture is refused."""
+    from tiktok_techjam_2026_track3_amd import GraphedForward, SelfAttention
+    w = W.CONFIGS[name].scaled(1, 128 if name == "C1" else 256)
+    params = W.round_params(W.make_params(w), w.dtype)
+    mod = SelfAttention(w.d_model, w.heads)
+    mod.load_state_dict(params)
+    mod = mod.to(device=gpu, dtype=w.dtype)
+    norm = torch.nn.LayerNorm(w.d_model).to(device=gpu, dtype=w.dtype) if half else None
+    mask = torch.ones(w.batch, w.seq, dtype=torch.bool, device=gpu) if masked else None
+    if masked:
+        mask[:, w.seq - 5:] = False
+    gf = GraphedForward(mod, W.make_input(w, 40).to(gpu), mask, w.causal, norm=norm)
+    with torch.inference_mode():
+        for seed in (41, 42, 43):
+            x = W.make_input(w, seed).to(gpu)
+            got = gf(x, mask)
+            noise = torch.randn(257, 129, device=gpu).sum()   # eager work between replays
+            torch.cuda.synchronize()
+            want = mod.forward_residual(x, norm, mask, w.causal) if half else mod(x, mask, w.causal)
+            torch.cuda.synchronize()
+            assert torch.isfinite(noise)
+            assert torch.equal(got, want), f"replay for seed {seed} differs from eager"
+        with torch.no_grad():
+            mod.out_proj.bias.add_(1.0)
+        with pytest.raises(RuntimeError):
+            gf(x, mask)

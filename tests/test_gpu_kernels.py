@@ -66,18 +66,19 @@ def test_linear_error_bound(gpu, dtype, out_dtype, M, N, K):
     assert _report("linear", err, bound) <= 1.0
 
 
-def test_linear_strided_input_and_row_mask(gpu):
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_linear_strided_input_and_row_mask(gpu, dtype):
     ops = _ops()
     M, N, K = 200, 96, 64
-    big = _rand((M, 3 * K), torch.float16, 4)
+    big = _rand((M, 3 * K), dtype, 4)
     x = big[:, K:2 * K]                        # row stride 3K, unit column stride
-    w = _rand((N, K), torch.float16, 5, scale=0.125)
+    w = _rand((N, K), dtype, 5, scale=0.125)
     b = _rand((N,), torch.float32, 6)
     rows = torch.rand(M, generator=torch.Generator().manual_seed(7)) > 0.3
     out = ops.linear(big.to(gpu)[:, K:2 * K], w.to(gpu), b.to(gpu), row_valid=rows.to(gpu)).cpu()
     ref = x.double() @ w.double().T + b.double()
     assert torch.all(out[~rows] == 0)
-    bound = UNIT[torch.float16] * ref.abs() + 4 * K * 2.0 ** -24 * (x.double().abs() @ w.double().abs().T) + 1e-7
+    bound = UNIT[dtype] * ref.abs() + 4 * K * 2.0 ** -24 * (x.double().abs() @ w.double().abs().T) + 1e-7
     assert ((out.double() - ref).abs()[rows] <= bound[rows]).all()
 
 
@@ -170,9 +171,10 @@ def test_attention_key_mask(gpu, dtype, causal):
     _attn_check(gpu, dtype, B, 2, S, S, 64, causal, key_valid=mask, seed=31)
 
 
-def test_attention_fully_masked_batch_gives_nan(gpu):
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+def test_attention_fully_masked_batch_gives_nan(gpu, dtype):
     ops = _ops()
-    q = torch.randn(2, 70, 1, 64, dtype=torch.float16, device=gpu)
+    q = torch.randn(2, 70, 1, 64, dtype=dtype, device=gpu)
     mask = torch.ones(2, 70, dtype=torch.bool, device=gpu)
     mask[1] = False
     out = ops.attention(q, q, q, key_valid=mask).cpu()

@@ -32,6 +32,13 @@ def test_cpu_forward_raises_instead_of_falling_back():
         mod(torch.randn(1, 8, 16))
 
 
+def test_graphed_forward_refuses_cpu_input():
+    from tiktok_techjam_2026_track3_amd import GraphedForward
+    mod = SelfAttention(64, 4)
+    with pytest.raises(RuntimeError, match="GPU"):
+        GraphedForward(mod, torch.zeros(1, 8, 64))
+
+
 def test_load_state_dict_and_apply_drop_derived_caches():
     mod = SelfAttention(32, 4)
     mod.__dict__["_mi355_pack"] = object()

@@ -5,16 +5,18 @@ Public API:
   build, swap_attention, swap_blocks,
   make_user_optimized_transformer       the reference's plugin insertion points (swap_blocks: the
                                         attention half of each block fused)
+  GraphedForward                        whole-forward graph capture / replay (small-shape latency)
   ops                                   torch wrappers of the C-ABI kernels
   workloads                             the measured configurations and seeded inputs
 """
 from .attention import Int8SelfAttention, SelfAttention
 from .plugin import build, make_user_optimized_transformer, swap_attention, swap_blocks
+from .graph import GraphedForward
 from . import ops, workloads
 
 BaselineSelfAttention = SelfAttention  # the reference's class name
 
 __all__ = [
     "SelfAttention", "Int8SelfAttention", "BaselineSelfAttention", "build", "swap_attention",
-    "make_user_optimized_transformer", "swap_blocks", "ops", "workloads",
+    "make_user_optimized_transformer", "swap_blocks", "GraphedForward", "ops", "workloads",
 ]

@@ -42,16 +42,31 @@ struct AttnArgs {
 
 constexpr float NEG_INF = -__builtin_huge_valf();
 
-// Work-group -> (query tile, head, batch). Non-causal grids are (q tiles, H, B). Causal grids are
-// 1-D and issued longest-first over the whole launch: every (batch, head)'s last query tile, then
-// every second-to-last one, ... (a query tile's work grows with its index), so no long tile is
-// left for the end. Consecutive work-groups are different heads; those of one head are H*B apart.
+// Work-group -> (query tile, head, batch).
+// Non-causal grids are 1-D and XCD-aware: the dispatcher deals work-groups round-robin to the 8
+// XCDs (work-group w runs on XCD w % 8), so XCD x is given the contiguous logical range x*q ..
+// of (head, query tile) pairs, query tile fastest. The query tiles of one head then run on one
+// XCD and share its K/V through that XCD's L2 (dealt round-robin, every XCD would fetch every
+// head's K/V from the fabric). Launches too large for a 1-D dispatch use a (q tiles, H, B) grid.
+// Causal grids are 1-D and issued longest-first over the whole launch: every (batch, head)'s last
+// query tile, then every second-to-last one, ... (a query tile's work grows with its index), so
+// no long tile is left for the end. Consecutive work-groups are different heads; those of one
+// head are H*B apart (on one XCD when H*B is a multiple of 8).
 template <bool CAUSAL>
 MI355_DEVINL void tile_of_block(const AttnArgs& p, int& qt, int64_t& h, int64_t& b) {
   if constexpr (CAUSAL) {
     const int64_t lin = blockIdx.x, hb_n = p.H * p.B;
     qt = p.n_qtiles - 1 - static_cast<int>(lin / hb_n);
     const int64_t hb = lin % hb_n;
+    h = hb % p.H;
+    b = hb / p.H;
+  } else if (gridDim.y == 1 && gridDim.z == 1) {
+    const int64_t total = gridDim.x;
+    const int64_t q = total / 8, r = total % 8;
+    const int64_t x = blockIdx.x % 8, j = blockIdx.x / 8;
+    const int64_t logical = x * q + (x < r ? x : r) + j;
+    qt = static_cast<int>(logical % p.n_qtiles);
+    const int64_t hb = logical / p.n_qtiles;
     h = hb % p.H;
     b = hb / p.H;
   } else {
@@ -493,78 +508,174 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   }
 }
 
-// fp32: one query per lane, 64 queries per work-group, K/V tiles of 64 keys in LDS.
-template <int HD, bool CAUSAL, bool KMASK>
-__global__ __launch_bounds__(64) void attn_fwd_f32(AttnArgs p) {
-  constexpr int BN = 64;
-  __shared__ float ks[BN][HD];
-  __shared__ float vs[BN][HD];
-  const int lane = threadIdx.x;
+// fp32 (VALU): four lanes per query, 16 queries per work-group of NWK waves, so the small fp32
+// problems (128 queries x 4 heads) still spread over many CUs. Lane 4*qq + ds holds dimensions
+// 16*j + 4*ds + (0..3) of query qq's row and of its output accumulator; a score is the sum of
+// the four lanes' partial dot products, exchanged inside the quad with two DPP adds (every lane
+// of the quad ends with the same bits). The keys are split into NWK contiguous ranges, one per
+// wave; each wave stages its keys 8 at a time in its own LDS slot (read back as broadcasts)
+// and fetches the next chunk (and its mask bytes) into registers while it computes the current
+// one, so no work-group barrier is needed in the loop. At the end the NWK partial states of a
+// query are merged through LDS: the common max M, l = sum_w l_w 2^((m_w - M) c), and the output.
+MI355_DEVINL float quad_sum(float v) {
+  // quad_perm [1,0,3,2] then [2,3,0,1]: after both, each lane holds (a0+a1)+(a2+a3) or its
+  // commuted form, which is the same value
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
+  return v;
+}
+
+template <int HD, bool CAUSAL, bool KMASK, int NWK>
+__global__ __launch_bounds__(64 * NWK) void attn_fwd_f32(AttnArgs p) {
+  constexpr int NJ = HD / 16;           // 16-byte pieces of a row per lane
+  // keys per staged chunk and per softmax block (head_dim 128: 4, which keeps the chunk's K
+  // reads the compiler hoists within the register budget)
+  constexpr int KB = HD == 64 ? 8 : 4;
+  constexpr int CH = KB * HD / 4;       // 16-byte pieces of one chunk's K (or V) rows
+  constexpr int PL = CH / 64;           // pieces per lane
+  static_assert(CH % 64 == 0, "chunk pieces per lane");
+  // per wave: K and V pieces of one chunk (the loop), reused as the merge buffer (NJ x 64 pieces
+  // per wave) after it
+  constexpr int SLOT = 2 * CH > NJ * 64 ? 2 * CH : NJ * 64;
+  __shared__ f32x4 lds[NWK][SLOT];
+  __shared__ float stat[NWK][2][64];
+  const int lane = threadIdx.x & 63;
+  const int qq = lane >> 2, ds = lane & 3;
+  const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   int qt;
   int64_t h, b;
   tile_of_block<CAUSAL>(p, qt, h, b);
-  const int64_t q_wg = static_cast<int64_t>(qt) * 64;
-  const int64_t qi = q_wg + lane;
-  const float* Qb = static_cast<const float*>(p.q) + b * p.qs0 + h * p.qs2;
-  const float* Kb = static_cast<const float*>(p.k) + b * p.ks0 + h * p.ks2;
-  const float* Vb = static_cast<const float*>(p.v) + b * p.vs0 + h * p.vs2;
-  const uint8_t* kvb = KMASK ? p.kv + b * p.kv_sb : nullptr;
+  const int q_wg = qt * 16;
+  const int qi = q_wg + qq;
+  const int sq = static_cast<int>(p.Sq), sk = static_cast<int>(p.Sk);
+  const float* __restrict__ Qb = static_cast<const float*>(p.q) + b * p.qs0 + h * p.qs2;
+  const float* __restrict__ Kb = static_cast<const float*>(p.k) + b * p.ks0 + h * p.ks2;
+  const float* __restrict__ Vb = static_cast<const float*>(p.v) + b * p.vs0 + h * p.vs2;
+  const uint8_t* __restrict__ kvb = KMASK ? p.kv + b * p.kv_sb : nullptr;
 
-  float q[HD], acc[HD];
+  f32x4 q[NJ], acc[NJ];
 #pragma unroll
-  for (int d = 0; d < HD; ++d) {
-    q[d] = qi < p.Sq ? Qb[qi * p.qs1 + d] : 0.f;
-    acc[d] = 0.f;
+  for (int j = 0; j < NJ; ++j) {
+    q[j] = qi < sq ? *reinterpret_cast<const f32x4*>(Qb + static_cast<int64_t>(qi) * p.qs1 + 16 * j + 4 * ds)
+                   : f32x4{0.f, 0.f, 0.f, 0.f};
+    acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   float m = NEG_INF, l = 0.f;
-  const int64_t kend = CAUSAL ? ((q_wg + 64) < p.Sk ? (q_wg + 64) : p.Sk) : p.Sk;
-  for (int64_t k0 = 0; k0 < kend; k0 += BN) {
-    __syncthreads();
-    for (int idx = lane; idx < BN * HD / 4; idx += 64) {
-      const int key = idx / (HD / 4), c4 = idx % (HD / 4);
-      f32x4 kv4 = {0.f, 0.f, 0.f, 0.f}, vv4 = {0.f, 0.f, 0.f, 0.f};
-      if (k0 + key < p.Sk) {
-        kv4 = *reinterpret_cast<const f32x4*>(Kb + (k0 + key) * p.ks1 + 4 * c4);
-        vv4 = *reinterpret_cast<const f32x4*>(Vb + (k0 + key) * p.vs1 + 4 * c4);
-      }
-      *reinterpret_cast<f32x4*>(&ks[key][4 * c4]) = kv4;
-      *reinterpret_cast<f32x4*>(&vs[key][4 * c4]) = vv4;
+  const int kend = CAUSAL ? __builtin_elementwise_min(q_wg + 16, sk) : sk;
+  const int per = (kend + NWK - 1) / NWK;
+  const int kbeg = wave * per;
+  const int kstop = __builtin_elementwise_min(kbeg + per, kend);
+  f32x4* kt = &lds[wave][0];
+  f32x4* vt = &lds[wave][CH];
+
+  // chunk fetch: lane i moves pieces i, i + 64, ... (rows past the range repeat its last row;
+  // their scores are discarded); the mask byte of key k0 + lane for lanes below KB
+  f32x4 nk[PL], nv[PL];
+  uint8_t nm = 1;
+  auto fetch = [&](int k0) {
+#pragma unroll
+    for (int t = 0; t < PL; ++t) {
+      const int i = lane + 64 * t;
+      const int kc = __builtin_elementwise_min(k0 + i / (HD / 4), kstop - 1), c4 = i % (HD / 4);
+      nk[t] = *reinterpret_cast<const f32x4*>(Kb + static_cast<int64_t>(kc) * p.ks1 + 4 * c4);
+      nv[t] = *reinterpret_cast<const f32x4*>(Vb + static_cast<int64_t>(kc) * p.vs1 + 4 * c4);
     }
-    __syncthreads();
-    for (int kb = 0; kb < BN; kb += 16) {
-      float s[16];
-      float mx = NEG_INF;
-      for (int kk = 0; kk < 16; ++kk) {
-        float d0 = 0.f;
+    if constexpr (KMASK) nm = lane < KB ? kvb[__builtin_elementwise_min(k0 + lane, kstop - 1)] : 0;
+  };
+  uint64_t kbits = ~0ull;
+  auto stage = [&]() {
 #pragma unroll
-        for (int d = 0; d < HD; ++d) d0 = __builtin_fmaf(q[d], ks[kb + kk][d], d0);
-        const int64_t key = k0 + kb + kk;
-        bool ok = key < p.Sk;
-        if (CAUSAL) ok = ok && key <= qi;
-        if (KMASK) ok = ok && kvb[key < p.Sk ? key : 0] != 0;
-        s[kk] = ok ? d0 : NEG_INF;
-        mx = fmaxf(mx, s[kk]);
-      }
-      const float m_new = fmaxf(m, mx);
-      const float alpha = (m == NEG_INF) ? 0.f : fast_exp2((m - m_new) * p.c);
-      const float mu = (m_new == NEG_INF) ? 0.f : m_new * p.c;
-      l *= alpha;
-#pragma unroll
-      for (int d = 0; d < HD; ++d) acc[d] *= alpha;
-      for (int kk = 0; kk < 16; ++kk) {
-        const float pk = fast_exp2(__builtin_fmaf(s[kk], p.c, -mu));
-        l += pk;
-#pragma unroll
-        for (int d = 0; d < HD; ++d) acc[d] = __builtin_fmaf(pk, vs[kb + kk][d], acc[d]);
-      }
-      m = m_new;
+    for (int t = 0; t < PL; ++t) {
+      kt[lane + 64 * t] = nk[t];
+      vt[lane + 64 * t] = nv[t];
     }
+    if constexpr (KMASK) kbits = __builtin_amdgcn_ballot_w64(nm != 0);
+  };
+  if (kbeg < kstop) {
+    fetch(kbeg);
+    stage();
   }
-  if (qi < p.Sq) {
-    float* Ob = static_cast<float*>(p.o) + b * p.os0 + qi * p.os1 + h * p.os2;
-    const float inv = 1.0f / l;
+  for (int k0 = kbeg; k0 < kstop; k0 += KB) {
+    const bool more = k0 + KB < kstop;
+    if (more) fetch(k0 + KB);
+    // the slot is written and read by this wave only, and LDS serves one wave's accesses in
+    // order: the fences only keep the compiler from moving the reads above the writes
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    float s[KB];
+    float mx = NEG_INF;
 #pragma unroll
-    for (int d = 0; d < HD; ++d) Ob[d] = acc[d] * inv;
+    for (int kk = 0; kk < KB; ++kk) {
+      float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const f32x4 kv = kt[kk * (HD / 4) + 4 * j + ds];
+        a0 = __builtin_fmaf(q[j][0], kv[0], a0);
+        a1 = __builtin_fmaf(q[j][1], kv[1], a1);
+        a2 = __builtin_fmaf(q[j][2], kv[2], a2);
+        a3 = __builtin_fmaf(q[j][3], kv[3], a3);
+      }
+      const float d0 = quad_sum((a0 + a1) + (a2 + a3));
+      const int key = k0 + kk;
+      bool ok = key < kstop;
+      if (CAUSAL) ok = ok && key <= qi;
+      if (KMASK) ok = ok && ((kbits >> kk) & 1ull);
+      s[kk] = ok ? d0 : NEG_INF;
+      mx = fmaxf(mx, s[kk]);
+    }
+    const float m_new = fmaxf(m, mx);
+    const float alpha = (m == NEG_INF) ? 0.f : fast_exp2((m - m_new) * p.c);
+    const float mu = (m_new == NEG_INF) ? 0.f : m_new * p.c;
+    l *= alpha;
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) acc[j] *= alpha;
+#pragma unroll
+    for (int kk = 0; kk < KB; ++kk) {
+      const float pk = fast_exp2(__builtin_fmaf(s[kk], p.c, -mu));
+      l += pk;
+#pragma unroll
+      for (int j = 0; j < NJ; ++j) {
+        const f32x4 vv = vt[kk * (HD / 4) + 4 * j + ds];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) acc[j][e] = __builtin_fmaf(pk, vv[e], acc[j][e]);
+      }
+    }
+    m = m_new;
+    __builtin_amdgcn_fence(__ATOMIC_SEQ_CST, "wavefront");
+    __builtin_amdgcn_wave_barrier();
+    if (more) stage();
+  }
+
+  // merge the NWK partial states of each query (the quad's four lanes hold the same m and l)
+  stat[wave][0][lane] = m;
+  stat[wave][1][lane] = l;
+  __syncthreads();  // also ends every wave's use of its staging slot
+  float M = NEG_INF;
+#pragma unroll
+  for (int w = 0; w < NWK; ++w) M = fmaxf(M, stat[w][0][lane]);
+  float L = 0.f;
+#pragma unroll
+  for (int w = 0; w < NWK; ++w) {
+    const float mw = stat[w][0][lane];
+    L += mw == NEG_INF ? 0.f : stat[w][1][lane] * fast_exp2((mw - M) * p.c);
+  }
+  const float scale = m == NEG_INF ? 0.f : fast_exp2((m - M) * p.c);
+  const float inv = 1.0f / L;  // all keys masked: 0/0 = NaN, as the reference's softmax
+#pragma unroll
+  for (int j = 0; j < NJ; ++j) lds[wave][j * 64 + lane] = acc[j] * scale;
+  __syncthreads();
+  if (qi < sq) {
+    float* Ob = static_cast<float*>(p.o) + b * p.os0 + static_cast<int64_t>(qi) * p.os1 + h * p.os2;
+    for (int j = wave; j < NJ; j += NWK) {
+      f32x4 sum = lds[0][j * 64 + lane];
+#pragma unroll
+      for (int w = 1; w < NWK; ++w) sum += lds[w][j * 64 + lane];
+      sum *= inv;
+      // the output pointer is 8-byte aligned: two 8-byte stores
+      typedef float f32x2 __attribute__((ext_vector_type(2)));
+      *reinterpret_cast<f32x2*>(Ob + 16 * j + 4 * ds) = f32x2{sum[0], sum[1]};
+      *reinterpret_cast<f32x2*>(Ob + 16 * j + 4 * ds + 2) = f32x2{sum[2], sum[3]};
+    }
   }
 }
 
@@ -630,11 +741,10 @@ int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
   a.n_qtiles = static_cast<int>((a.Sq + BM - 1) / BM);
   const dim3 block(NW * 64);
   dim3 grid(a.n_qtiles, static_cast<unsigned>(a.H), static_cast<unsigned>(a.B));
-  if (causal) {
-    const int64_t n = static_cast<int64_t>(a.n_qtiles) * a.H * a.B;
-    if (n * (NW * 64) > 0xffffffffLL) return MI355_E_BAD_SIZE;  // dispatch size is 32-bit
-    grid = dim3(static_cast<unsigned>(n), 1, 1);
-  }
+  const int64_t n = static_cast<int64_t>(a.n_qtiles) * a.H * a.B;
+  const bool flat = n * (NW * 64) <= 0xffffffffLL;  // dispatch size is 32-bit
+  if (causal && !flat) return MI355_E_BAD_SIZE;
+  if (flat) grid = dim3(static_cast<unsigned>(n), 1, 1);
   if (causal) {
     if (kmask) launch_one<T, HD, NW, QG, true, true>(a, grid, block, s);
     else launch_one<T, HD, NW, QG, true, false>(a, grid, block, s);
@@ -647,18 +757,22 @@ int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
 
 template <int HD>
 int launch_f32(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
+  constexpr int NWK = 8;  // waves (key ranges) per 16 queries
   AttnArgs a = a0;
-  a.n_qtiles = static_cast<int>((a.Sq + 63) / 64);
+  a.n_qtiles = static_cast<int>((a.Sq + 15) / 16);
+  if (static_cast<int64_t>(a.n_qtiles) * 64 * NWK > 0xffffffffLL) return MI355_E_BAD_SIZE;
   dim3 grid(a.n_qtiles, static_cast<unsigned>(a.H), static_cast<unsigned>(a.B));
+  const dim3 block(64 * NWK);
+  const int64_t n = static_cast<int64_t>(a.n_qtiles) * a.H * a.B;
+  const bool flat = n * 64 * NWK <= 0xffffffffLL;  // dispatch size is 32-bit
+  if (causal && !flat) return MI355_E_BAD_SIZE;
+  if (flat) grid = dim3(static_cast<unsigned>(n), 1, 1);
   if (causal) {
-    const int64_t n = static_cast<int64_t>(a.n_qtiles) * a.H * a.B;
-    if (n * 64 > 0xffffffffLL) return MI355_E_BAD_SIZE;
-    grid = dim3(static_cast<unsigned>(n), 1, 1);
-    if (kmask) hipLaunchKernelGGL((attn_fwd_f32<HD, true, true>), grid, dim3(64), 0, s, a);
-    else hipLaunchKernelGGL((attn_fwd_f32<HD, true, false>), grid, dim3(64), 0, s, a);
+    if (kmask) hipLaunchKernelGGL((attn_fwd_f32<HD, true, true, NWK>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_fwd_f32<HD, true, false, NWK>), grid, block, 0, s, a);
   } else {
-    if (kmask) hipLaunchKernelGGL((attn_fwd_f32<HD, false, true>), grid, dim3(64), 0, s, a);
-    else hipLaunchKernelGGL((attn_fwd_f32<HD, false, false>), grid, dim3(64), 0, s, a);
+    if (kmask) hipLaunchKernelGGL((attn_fwd_f32<HD, false, true, NWK>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_fwd_f32<HD, false, false, NWK>), grid, block, 0, s, a);
   }
   return static_cast<int>(hipGetLastError());
 }

@@ -423,6 +423,79 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
 #define MI355_GEMM_DIRECT 1
 #endif
 
+// Small fp32 problems (the fp32 configuration's projections are 128 x 768 x 256 and
+// 128 x 256 x 256): a 32 x 32 output tile per work-group whose NWS waves split K. With one wave
+// per tile a 32x32 fp32 MFMA tile costs K/2 MFMAs of 64 cycles in sequence; split NWS ways the
+// chain is NWS times shorter and NWS times more SIMDs share it. Fragments come straight from
+// global memory (lane (l32, g) reads 16 bytes of row l32 for chunk 2j + g; rows are K-major),
+// U chunk pairs per wave requested before the first MFMA. The NWS partial tiles are summed
+// through LDS in wave order (deterministic), then bias, row mask and residual are applied per
+// element as in gemm_kernel's epilogue and the tile is written row by row.
+template <int NWS>
+__global__ __launch_bounds__(64 * NWS) void gemm_f32_splitk(GemmArgs p) {
+  constexpr int U = 4;
+  constexpr int PITCH = 65;  // padded: the reduction reads 32 features of one token per half-wave
+  __shared__ float red[NWS][16][PITCH];
+  using MF = Mfma<float>;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int g = lane >> 5, l32 = lane & 31;
+  const int64_t ntm = (p.M + 31) / 32, ntn = (p.N + 31) / 32;
+  int64_t tmi, tni;
+  tile_coords(blockIdx.x, ntm, ntn, tmi, tni);
+  const int64_t m0 = tmi * 32, n0 = tni * 32;
+  const int64_t am = m0 + l32, wn = n0 + l32;
+  const bool a_ok = am < p.M, w_ok = wn < p.N;
+  const float* arow = static_cast<const float*>(p.A) + (a_ok ? am : 0) * p.lda;
+  const float* wrow = static_cast<const float*>(p.W) + (w_ok ? wn : 0) * p.ldw;
+  const int nchunk = static_cast<int>(p.K / 4);
+
+  // D = W_rows . A_rows^T: lane l keeps token l % 32 and features mfma_row(i, l)
+  typename MF::acc acc;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) acc[i] = 0.f;
+  // wave w takes chunk pairs w, w + NWS, w + 2 NWS, ...; half-wave g the pair's chunk g
+  for (int base = 2 * wave; base < nchunk; base += 2 * NWS * U) {
+    f32x4 fa[U], fw[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      const int c = base + u * 2 * NWS + g;
+      const bool in = c < nchunk;
+      fa[u] = (in && a_ok) ? *reinterpret_cast<const f32x4*>(arow + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      fw[u] = (in && w_ok) ? *reinterpret_cast<const f32x4*>(wrow + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int u = 0; u < U; ++u) acc = MF::mma(fw[u], fa[u], acc);
+  }
+#pragma unroll
+  for (int i = 0; i < 16; ++i) red[wave][i][lane] = acc[i];
+  __syncthreads();
+
+  // element (token m_loc, feature n_loc) lives in register i of lane l: n_loc = mfma_row(i, l)
+  for (int e = tid; e < 32 * 32; e += 64 * NWS) {
+    const int n_loc = e & 31, m_loc = e >> 5;
+    const int64_t m = m0 + m_loc, n = n0 + n_loc;
+    if (m >= p.M || n >= p.N) continue;
+    const int l = m_loc + 32 * ((n_loc >> 2) & 1), i = (n_loc >> 3) * 4 + (n_loc & 3);
+    float v = red[0][i][l];
+#pragma unroll
+    for (int w = 1; w < NWS; ++w) v += red[w][i][l];
+    if (p.bias) v = v + p.bias[n];
+    if (p.row_valid && p.row_valid[m] == 0) v = 0.f;
+    // residual read before the write of the same element: R may be C
+    if (p.R) v = v + static_cast<const float*>(p.R)[m * p.ldr + n];
+    static_cast<float*>(p.C)[m * p.ldc + n] = v;
+  }
+}
+
+int launch_gemm_f32_splitk(const GemmArgs& a, hipStream_t stream) {
+  constexpr int NWS = 8;
+  const int64_t tiles = ((a.M + 31) / 32) * ((a.N + 31) / 32);
+  const dim3 grid(static_cast<unsigned>(tiles)), block(64 * NWS);
+  hipLaunchKernelGGL((gemm_f32_splitk<NWS>), grid, block, 0, stream, a);
+  return static_cast<int>(hipGetLastError());
+}
+
 template <typename T, typename TO, int BM, int BN, int WM, int WN, bool INT8>
 int launch_gemm(const GemmArgs& a, hipStream_t stream) {
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
@@ -495,7 +568,15 @@ int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, cons
   switch (in_dtype) {
     case MI355_F16: return launch_by_out<_Float16, 256, 256, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
     case MI355_BF16: return launch_by_out<__bf16, 256, 256, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
-    default: return launch_gemm<float, float, 128, 128, 2, 2, false>(a, s);
+    default: {
+      // small problems (the fp32 configuration's projections are 128 x 768 and 128 x 256):
+      // 32 x 32 tiles with K split over 8 waves; mid-size ones 64 x 64 tiles
+      const int64_t tiles32 = ((a.M + 31) / 32) * ((a.N + 31) / 32);
+      const int64_t tiles128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
+      if (tiles32 <= 512) return launch_gemm_f32_splitk(a, s);
+      if (tiles128 < 64) return launch_gemm<float, float, 64, 64, 2, 2, false>(a, s);
+      return launch_gemm<float, float, 128, 128, 2, 2, false>(a, s);
+    }
   }
 }
 }  // namespace
