@@ -112,13 +112,31 @@ MI355_DEVINL float pair_max(float v) {
 // lgkmcnt(0) while the load is in flight, and adds vmcnt waits before transpose reads. Callers
 // order the data themselves (s_waitcnt vmcnt + a work-group barrier before the destination is
 // read) and never read a destination while its load is in flight. lds_addr must be wave-uniform.
+// An SALU write of M0 needs one wait state before a load with LDS=1 reads it (the s_nop 0 the
+// compiler also emits for its own LDS-DMA loads).
 MI355_DEVINL void dma_lds16(const void* gptr, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr),
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(gptr),
                "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory", "m0");
 }
 MI355_DEVINL void dma_lds1(const void* gptr, uint32_t lds_addr) {
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_ubyte %0, off" ::"v"(gptr),
+  asm volatile("s_mov_b32 m0, %1\n\ts_nop 0\n\tglobal_load_lds_ubyte %0, off" ::"v"(gptr),
+               "s"(__builtin_amdgcn_readfirstlane(lds_addr))
+               : "memory", "m0");
+}
+// Raw buffer resource (base, stride 0, `bytes` records, 32-bit data format) as four wave-uniform
+// dwords: loads at or past `bytes` (voffset + soffset + instruction offset) return zeros.
+MI355_DEVINL u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  const auto u = [](uint32_t v) { return static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(v)); };
+  return u32x4{u(static_cast<uint32_t>(a)), u(static_cast<uint32_t>(a >> 32) & 0xffffu), u(bytes),
+               0x00020000u};
+}
+// Buffer load straight into LDS (16 bytes per lane from rsrc base + voffset + soffset, landing
+// at LDS lds_addr + 16 lane), issued from inline assembly for the reason given above.
+MI355_DEVINL void buffer_dma_lds16(u32x4 rsrc, uint32_t voffset, uint32_t soffset, uint32_t lds_addr) {
+  asm volatile("s_mov_b32 m0, %3\n\ts_nop 0\n\tbuffer_load_dwordx4 %0, %1, %2 offen lds" ::"v"(voffset),
+               "s"(rsrc), "s"(__builtin_amdgcn_readfirstlane(soffset)),
                "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory", "m0");
 }

@@ -9,9 +9,21 @@
 // epilogue stages the finished tile in LDS and writes it back in 16-byte row chunks.
 #include "common.h"
 
-// interleave the LDS fragment reads of k-slice j+1 with the MFMAs of slice j (scheduler hints)
+// interleave the LDS fragment reads of k-slice j+1 with the MFMAs of slice j: 1 = scheduler
+// hints, 2 = explicit issue order (MFMA, read, MFMA, read, ... fenced by sched_barrier);
+// measured on the projection shapes: 2 is 3-5% faster than 1
 #ifndef MI355_GEMM_SCHED
-#define MI355_GEMM_SCHED 1
+#define MI355_GEMM_SCHED 2
+#endif
+// with the explicit issue order: alternate the issue priority of the two waves of a SIMD
+// (1: per half K step, 2: per k-slice). Without it the older wave of each SIMD finishes its
+// step's MFMAs ~1000 cycles before the younger one, which then runs alone on the MFMA pipe.
+#ifndef MI355_GEMM_PP
+#define MI355_GEMM_PP 1
+#endif
+// with the explicit issue order: spread each step's LDS-DMA loads over its MFMAs
+#ifndef MI355_GEMM_SPREAD
+#define MI355_GEMM_SPREAD 1
 #endif
 
 namespace {
@@ -50,6 +62,11 @@ MI355_DEVINL int swzc(int r) {
     return ((r >> 1) & 3) ^ ((r >> 3) & 1);
 }
 
+// minimum waves per SIMD for work-groups of at most 4 waves (2: two work-groups share a CU)
+#ifndef MI355_GEMM_WPE
+#define MI355_GEMM_WPE 2
+#endif
+
 // direct (LDS-DMA) path: 16-byte chunks per row per K step, and depth of the LDS ring. Measured
 // on the projection shapes: 8 chunks x 2 stages beats 4 chunks x 3-4 stages (the shorter K step
 // doubles the barriers per tile)
@@ -83,7 +100,7 @@ MI355_DEVINL void tile_coords(int64_t pid, int64_t ntm, int64_t ntn, int64_t& tm
 // slots of CHK chunks per row. Requires K % BK == 0. Otherwise a register-staged, double-
 // buffered loader with bounds checks runs (8 chunks per row).
 template <typename T, typename TO, int BM, int BN, int WM, int WN, bool INT8, bool DIRECT>
-__global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
+__global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) void gemm_kernel(GemmArgs p) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
   using acc_t = typename MF::acc;
@@ -187,16 +204,20 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
     doff[i] = row < BM ? static_cast<uint32_t>(row) * a_pitch + c * 16u
                        : static_cast<uint32_t>(row - BM) * w_pitch + c * 16u;
   }
-  auto load_direct = [&](int s, int64_t k0) {
+  // issued from inline assembly (buffer_dma_lds16): the compiler then keeps precise LDS wait
+  // counts for the fragment reads instead of draining every outstanding load before each one
+  const u32x4 a_rsrc = buffer_rsrc(a_base, a_bytes), w_rsrc = buffer_rsrc(w_base, w_bytes);
+  auto load_one = [&](int s, int64_t k0, int i) {
     const uint32_t so = static_cast<uint32_t>(k0) * ES;
+    const int blk = wv + i * NWAVE;
+    if (i < (BM / RBK) / NWAVE)
+      buffer_dma_lds16(a_rsrc, doff[i], so, lds_addr_of(&lds[s][blk * 64]));
+    else
+      buffer_dma_lds16(w_rsrc, doff[i], so, lds_addr_of(&lds[s][blk * 64]));
+  };
+  auto load_direct = [&](int s, int64_t k0) {
 #pragma unroll
-    for (int i = 0; i < NLD; ++i) {
-      const int blk = wv + i * NWAVE;
-      if (i < (BM / RBK) / NWAVE)
-        buffer_load_lds16(a_base, a_bytes, &lds[s][blk * 64], doff[i], so);
-      else
-        buffer_load_lds16(w_base, w_bytes, &lds[s][blk * 64], doff[i], so);
-    }
+    for (int i = 0; i < NLD; ++i) load_one(s, k0, i);
   };
 
   const int nk = static_cast<int>((p.K + BK - 1) / BK);
@@ -204,25 +225,69 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
 
   // MFMAs of one K step from ring slot `cur`; the fragments of k-slice j+1 are read while the
   // MFMAs of slice j run (two register sets)
-  auto compute = [&](const int cur) {
+  // dma_slot >= 0: the NLD loads of K offset dma_k0 into that ring slot are issued between the
+  // MFMAs of the first half of the step (one after every DMA_EVERY-th MFMA), so the work-group's
+  // loads do not reach the memory system as one burst after the barrier
+  constexpr int DMA_EVERY = (TM * TN * (CHK / 2)) / (2 * NLD) > 0 ? (TM * TN * (CHK / 2)) / (2 * NLD) : 1;
+  static_assert(NLD * DMA_EVERY <= TM * TN * (CHK / 2), "every load of a step has an MFMA slot");
+  auto compute = [&](const int cur, const int dma_slot = -1, const int64_t dma_k0 = 0) {
     frag fa[2][TM], fb[2][TN];
-    auto read_frags = [&](int j, int buf) {
+    auto read_frag = [&](int j, int buf, int f) {
       const int c = 2 * j + g;
-#pragma unroll
-      for (int a = 0; a < TM; ++a) {
-        const int row = wm * WTM + a * 32 + l32;
-        fa[buf][a] = __builtin_bit_cast(frag, lds[cur][row * CHK + (c ^ swzc<CHK>(row))]);
-      }
-#pragma unroll
-      for (int b = 0; b < TN; ++b) {
-        const int row = wn * WTN + b * 32 + l32;
-        fb[buf][b] = __builtin_bit_cast(frag, lds[cur][(BM + row) * CHK + (c ^ swzc<CHK>(row))]);
+      if (f < TM) {
+        const int row = wm * WTM + f * 32 + l32;
+        fa[buf][f] = __builtin_bit_cast(frag, lds[cur][row * CHK + (c ^ swzc<CHK>(row))]);
+      } else {
+        const int row = wn * WTN + (f - TM) * 32 + l32;
+        fb[buf][f - TM] = __builtin_bit_cast(frag, lds[cur][(BM + row) * CHK + (c ^ swzc<CHK>(row))]);
       }
     };
-    read_frags(0, 0);
+#pragma unroll
+    for (int f = 0; f < TM + TN; ++f) read_frag(0, 0, f);
 #pragma unroll
     for (int j = 0; j < CHK / 2; ++j) {
-      if (j + 1 < CHK / 2) read_frags(j + 1, (j + 1) & 1);
+#if MI355_GEMM_SCHED == 2
+      // explicit issue order: MFMA i of slice j, then fragment i of slice j+1 (sched_barrier
+      // fences keep the compiler from pairing each read with the MFMA that consumes it)
+#if MI355_GEMM_PP
+      {
+        // the two waves sharing a SIMD (w and w + NWAVE/2) take turns at the higher issue
+        // priority, so neither runs far ahead and leaves the other alone on the MFMA pipe
+        const int half = MI355_GEMM_PP == 1 ? (j >= CHK / 4) : (j & 1);
+        if ((wv >= NWAVE / 2) != (half != 0))
+          __builtin_amdgcn_s_setprio(1);
+        else
+          __builtin_amdgcn_s_setprio(0);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+#endif
+      // (a wave tile of one MFMA block has more fragments per slice than MFMAs: the loop runs
+      // to the larger count, issuing MFMAs only for the first TM * TN positions)
+      constexpr int NPOS = TM * TN > TM + TN ? TM * TN : TM + TN;
+#pragma unroll
+      for (int i = 0; i < NPOS; ++i) {
+        if (i < TM * TN) {
+          const int a = i / TN, b = i % TN;
+          acc[a][b] = MF::mma(fb[j & 1][b], fa[j & 1][a], acc[a][b]);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+        if constexpr (DIRECT) {
+          const int q = j * TM * TN + i;  // MFMA index within the step
+          if (i < TM * TN && dma_slot >= 0 && q % DMA_EVERY == DMA_EVERY - 1 && q / DMA_EVERY < NLD) {
+            load_one(dma_slot, dma_k0, q / DMA_EVERY);
+            __builtin_amdgcn_sched_barrier(0);
+          }
+        }
+        if (j + 1 < CHK / 2 && i < TM + TN) {
+          read_frag(j + 1, (j + 1) & 1, i);
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+#else
+      if (j + 1 < CHK / 2) {
+#pragma unroll
+        for (int f = 0; f < TM + TN; ++f) read_frag(j + 1, (j + 1) & 1, f);
+      }
 #pragma unroll
       for (int a = 0; a < TM; ++a)
 #pragma unroll
@@ -237,6 +302,7 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
         }
         __builtin_amdgcn_sched_group_barrier(0x008, TM * TN - (TM + TN), 0);
       }
+#endif
 #endif
     }
   };
@@ -265,8 +331,12 @@ __global__ __launch_bounds__(WM* WN * 64) void gemm_kernel(GemmArgs p) {
     __syncthreads();
     auto step = [&](const int kt, const int slot) {
       const int kl = kt + NST - 1;
+#if MI355_GEMM_SCHED == 2 && MI355_GEMM_SPREAD
+      compute(slot, kl < nk ? (slot + NST - 1) % NST : -1, static_cast<int64_t>(kl) * BK);
+#else
       if (kl < nk) load_direct((slot + NST - 1) % NST, static_cast<int64_t>(kl) * BK);
       compute(slot);
+#endif
       if (kl < nk)
         __builtin_amdgcn_s_waitcnt(WAIT_FULL);
       else
@@ -518,6 +588,12 @@ int launch_gemm(const GemmArgs& a, hipStream_t stream) {
 }  // namespace
 
 // 16-bit / int8 work-group tile 256 x 256; wave grid overridable at build time
+#ifndef MI355_GEMM_BM
+#define MI355_GEMM_BM 256
+#endif
+#ifndef MI355_GEMM_BN
+#define MI355_GEMM_BN 256
+#endif
 #ifndef MI355_GEMM_WM
 #define MI355_GEMM_WM 4
 #endif
@@ -566,8 +642,8 @@ int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, cons
   a.out_dtype = out_dtype;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (in_dtype) {
-    case MI355_F16: return launch_by_out<_Float16, 256, 256, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
-    case MI355_BF16: return launch_by_out<__bf16, 256, 256, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
+    case MI355_F16: return launch_by_out<_Float16, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
+    case MI355_BF16: return launch_by_out<__bf16, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
     default: {
       // small problems (the fp32 configuration's projections are 128 x 768 and 128 x 256):
       // 32 x 32 tiles with K split over 8 waves; mid-size ones 64 x 64 tiles
@@ -626,5 +702,5 @@ extern "C" int mi355_gemm_i8(const int8_t* A, const int8_t* W, const float* s_a,
   a.N = N;
   a.K = K;
   a.out_dtype = out_dtype;
-  return launch_by_out<int8_t, 256, 256, MI355_GEMM_WM, MI355_GEMM_WN, true>(a, static_cast<hipStream_t>(stream));
+  return launch_by_out<int8_t, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, true>(a, static_cast<hipStream_t>(stream));
 }
