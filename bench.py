@@ -50,6 +50,11 @@ def parse_args():
                          "(torch_transformer_benchmark.py:139): LayerNorm kernel, QKV projection, "
                          "attention, out projection with the residual add in its epilogue "
                          "(16-bit / fp32 configurations)")
+    ap.add_argument("--full-block", action="store_true",
+                    help="time one whole transformer block (torch_transformer_benchmark.py:134-145) "
+                         "on the kernels: norm1, QKV, attention, out + residual, norm2, ffn_in + "
+                         "GELU, ffn_out + residual + row mask; ffn_dim = 4 d_model (16-bit / fp32 "
+                         "configurations)")
     ap.add_argument("--graph", action="store_true",
                     help="time replays of one step captured in a HIP graph (torch.cuda.CUDAGraph): "
                          "no per-kernel host launch cost; the per-stage breakdown still comes from "
@@ -72,7 +77,7 @@ def measured_traffic(config: str, stage: str):
             rec = json.load(f).get(config)
     except (OSError, ValueError):
         return None
-    if not rec or STAGE_KERNEL[stage] not in rec.get("kernel", ""):
+    if not rec or stage not in STAGE_KERNEL or STAGE_KERNEL[stage] not in rec.get("kernel", ""):
         return None
     return rec["bytes_per_launch"]
 
@@ -167,16 +172,19 @@ def cpu_baseline(w, budget_s: float) -> dict:
 
 # ------------------------------------------------------------------------------ gpu measure
 def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
-            half: bool = False, graph: bool = False) -> dict:
+            half: bool = False, graph: bool = False, full: bool = False) -> dict:
     import torch
-    from tiktok_techjam_2026_track3_amd import Int8SelfAttention, SelfAttention
+    import torch.nn.functional as F
+    from tiktok_techjam_2026_track3_amd import Int8SelfAttention, SelfAttention, TransformerBlock
     from tiktok_techjam_2026_track3_amd import workloads as W
+    from tiktok_techjam_2026_track3_amd.transformer import block_forward
 
     w = W.CONFIGS[name]
     dev = torch.device("cuda:0")
     params = W.make_params(w)
-    if half and w.int8:
-        raise ValueError("--attention-half covers the 16-bit / fp32 configurations")
+    if (half or full) and w.int8:
+        raise ValueError("--attention-half / --full-block cover the 16-bit / fp32 configurations")
+    ffn_dim = 4 * w.d_model
     if w.int8:
         mod = Int8SelfAttention(w.d_model, w.heads)
         mod.load_state_dict(params)
@@ -189,7 +197,16 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         stages = ["qkv", "attn", "out"]
     x = W.make_input(w, W.TIMING_SEED, device="cuda")
     valid = torch.ones(w.batch, w.seq, dtype=torch.bool, device=dev)
-    if half:
+    if full:
+        torch.manual_seed(W.WEIGHT_SEED + 1)  # norm / FFN parameters: nn.LayerNorm / nn.Linear init
+        blk = TransformerBlock(w.d_model, w.heads, ffn_dim)
+        blk.attention.load_state_dict(params)
+        blk = blk.to(device=dev, dtype=w.dtype).eval()
+        stages = ["norm", "qkv", "attn", "out", "norm2", "ffn_in", "ffn_out"]
+
+        def step(marks=None):
+            return block_forward(blk, x, valid, w.causal, marks=marks)
+    elif half:
         norm = torch.nn.LayerNorm(w.d_model).to(device=dev, dtype=w.dtype)
         stages = ["norm"] + stages
 
@@ -234,6 +251,22 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
             u1.record()
             torch.cuda.synchronize()
             unfused_ms = u0.elapsed_time(u1) / steps
+        if full:
+            # the FFN half as torch ops (the reference's code) after the fused attention half
+            def torch_ffn_block():
+                x1 = blk.attention.forward_residual(x, blk.norm1, valid, w.causal)
+                y = x1 + blk.ffn_out(F.gelu(blk.ffn_in(blk.norm2(x1)), approximate="none"))
+                return y.masked_fill(~valid[..., None], 0)
+            for _ in range(max(3, warmup // 4)):
+                torch_ffn_block()
+            torch.cuda.synchronize()
+            u0, u1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            u0.record()
+            for _ in range(steps):
+                torch_ffn_block()
+            u1.record()
+            torch.cuda.synchronize()
+            unfused_ms = u0.elapsed_time(u1) / steps
     ms_step = start.elapsed_time(end) / steps
     eager_ms = ms_step
     if graph:
@@ -257,17 +290,25 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
             g1.record()
             torch.cuda.synchronize()
         ms_step = g0.elapsed_time(g1) / steps
-    fl = w.flops()
+    fl = dict(w.flops())
     by = dict(w.bytes())
-    if half:
+    if half or full:
         act = w.tokens * w.d_model * x.element_size()
         by["norm"] = 2 * act                      # read x, write norm1(x)
         by["out"] = by["out"] + act               # the residual read in the epilogue
+    if full:
+        e = x.element_size()
+        T, d = w.tokens, w.d_model
+        fl["ffn_in"] = 2.0 * T * d * ffn_dim
+        fl["ffn_out"] = 2.0 * T * ffn_dim * d
+        by["norm2"] = 2 * act
+        by["ffn_in"] = (T * d + ffn_dim * d) * e + 4 * ffn_dim + T * ffn_dim * e
+        by["ffn_out"] = (T * ffn_dim + d * ffn_dim) * e + 4 * d + 2 * T * d * e
     stage_ms = {}
     for i, s in enumerate(stages):
         nxt = marks_order[i + 1]
         stage_ms[s] = sum(events[k][s].elapsed_time(events[k][nxt]) for k in range(steps)) / steps
-    total_ops = fl["qkv"] + fl["attn"] + fl["out"]
+    total_ops = fl["qkv"] + fl["attn"] + fl["out"] + fl.get("ffn_in", 0.0) + fl.get("ffn_out", 0.0)
     dt = DTYPE_NAME[str(w.dtype)]
     stage_report = {}
     for s, ms in stage_ms.items():
@@ -285,7 +326,8 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         kdt = "fp16" if (w.int8 or w.dtype == torch.bfloat16) else dt
         peak = PEAKS_TFLOPS[kdt]
     achieved = fl[dom] / stage_ms[dom] / 1e9
-    kernel_name = {"qkv": "gemm (QKV projection)", "attn": "attn_fwd", "out": "gemm (out projection)"}[dom]
+    kernel_name = {"qkv": "gemm (QKV projection)", "attn": "attn_fwd", "out": "gemm (out projection)",
+                   "ffn_in": "gemm (ffn_in + GELU)", "ffn_out": "gemm (ffn_out + residual)"}[dom]
     result = {
         "metric": "attention-block ms/iter + TFLOP/s (% of MFMA peak) per config, 1 MI355X",
         "value": round(total_ops / ms_step / 1e9, 3),
@@ -300,7 +342,9 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         "dtype": ("int8+fp16" if w.int8 else ("bf16 projections, fp16 SDPA core" if w.dtype == torch.bfloat16 else dt)),
         "data": "synthetic (seeded N(0,1) inputs, configuration weight init)",
         "config": {"workload": f"{w.name}: {w.description}"
-                               + (" + norm1 and residual (attention half of the block)" if half else ""),
+                               + (" + norm1 and residual (attention half of the block)" if half else "")
+                               + (f" + norm1/norm2, residuals, FFN {w.d_model}->{ffn_dim}->{w.d_model} "
+                                  "with exact GELU (whole transformer block)" if full else ""),
                    "batch": w.batch, "seq_len": w.seq,
                    "d_model": w.d_model, "heads": w.heads, "head_dim": w.head_dim,
                    "causal": w.causal, "parallelism": "none (1 GPU)"},
@@ -312,7 +356,8 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         "wall_s": round(wall, 3),
         "launch": "graph replay" if graph else "eager",
         **({"eager_ms_per_step": round(eager_ms, 5)} if graph else {}),
-        **({"unfused_half_ms_per_step": round(unfused_ms, 5)} if unfused_ms is not None else {}),
+        **({("torch_ffn_block_ms_per_step" if full else "unfused_half_ms_per_step"): round(unfused_ms, 5)}
+           if unfused_ms is not None else {}),
         "warmup_steps_run": n_warm,
         "warmup_s": round(warm_s, 3),
     }
@@ -342,7 +387,7 @@ def main() -> int:
             return 2
         log(f"[bench] {name}: warmup {args.warmup}, steps {args.steps}")
         res = measure(name, args.steps, args.warmup, args.min_warmup_s, args.attention_half,
-                      args.graph)
+                      args.graph, args.full_block)
         log(f"[bench] {name}: {res['ms_per_step']} ms/step, {res['value']} {res['unit']}")
         if not args.no_cpu_baseline:
             log(f"[bench] {name}: cpu baseline (budget {args.cpu_budget}s)")

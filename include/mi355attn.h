@@ -135,6 +135,41 @@ int mi355_gemm_bias_residual(int in_dtype, int out_dtype, const void* A, int64_t
                              int64_t ldc, int64_t M, int64_t N, int64_t K, const uint8_t* row_valid,
                              void* stream);
 
+/*
+ * FFN input projection with the exact GELU fused into its epilogue:
+ *   C = out_dtype( gelu( out_dtype(A · W^T + bias) ) ),  gelu(x) = x * 0.5 * (1 + erf(x / sqrt 2))
+ * i.e. `F.gelu(self.ffn_in(h), approximate="none")` of BaselineTransformerBlock.forward
+ * (torch_transformer_benchmark.py:141; ffn_in = nn.Linear(d_model, ffn_dim), :131): the linear
+ * output is rounded to out_dtype (the nn.Linear output tensor), GELU is evaluated in fp32 on it and
+ * rounded again. Arguments as mi355_gemm_bias without the row mask.
+ */
+int mi355_gemm_bias_gelu(int in_dtype, int out_dtype, const void* A, int64_t lda, const void* W,
+                         int64_t ldw, const float* bias, void* C, int64_t ldc, int64_t M, int64_t N,
+                         int64_t K, void* stream);
+
+/*
+ * FFN output projection with the residual add and the block's trailing row mask fused:
+ *   C = R + out_dtype(A · W^T + bias) for rows with row_valid[m] != 0, C = 0 for the others
+ * i.e. `x = x + self.ffn_out(...)` followed by `x.masked_fill(~valid_token_mask[..., None], 0)`
+ * (torch_transformer_benchmark.py:141-144; ffn_out = nn.Linear(ffn_dim, d_model), :132).
+ * row_valid may be NULL (no row is masked). Otherwise as mi355_gemm_bias_residual.
+ */
+int mi355_gemm_bias_residual_zero_masked(int in_dtype, int out_dtype, const void* A, int64_t lda,
+                                         const void* W, int64_t ldw, const float* bias,
+                                         const void* R, int64_t ldr, void* C, int64_t ldc,
+                                         int64_t M, int64_t N, int64_t K,
+                                         const uint8_t* row_valid, void* stream);
+
+/*
+ * mi355_layernorm with a row mask: rows with row_valid[m] == 0 are written as zeros. Replaces
+ * `self.norm2(x)` (torch_transformer_benchmark.py:141, row_valid NULL) and the model's
+ * `self.final_norm(x)` followed by `x.masked_fill(~valid_token_mask[..., None], 0)` (:168-171).
+ * row_valid may be NULL. Otherwise as mi355_layernorm.
+ */
+int mi355_layernorm_masked(int dtype, const void* X, int64_t ldx, const void* gamma, const void* beta,
+                           float eps, void* Y, int64_t ldy, int64_t M, int64_t K,
+                           const uint8_t* row_valid, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -40,6 +40,16 @@ _SIGNATURES = {
         C.c_int,
         [C.c_int, C.c_int, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P],
     ),
+    "mi355_gemm_bias_gelu": (
+        C.c_int, [C.c_int, C.c_int, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64, _P],
+    ),
+    "mi355_gemm_bias_residual_zero_masked": (
+        C.c_int,
+        [C.c_int, C.c_int, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P],
+    ),
+    "mi355_layernorm_masked": (
+        C.c_int, [C.c_int, _P, _I64, _P, _P, C.c_float, _P, _I64, _I64, _I64, _P, _P],
+    ),
     "mi355_gemm_i8": (
         C.c_int,
         [_P, _P, _P, _P, _P, C.c_int, _P, _I64, _P, _I64, _I64, _I64, _P, _P],

@@ -41,7 +41,41 @@ struct GemmArgs {
   int64_t lda, ldw, ldc, ldr;
   int64_t M, N, K;
   int out_dtype;
+  int epi;  // EPI_* flags
 };
+
+// Epilogue options beyond bias / row mask / residual:
+//   EPI_GELU         y = gelu(round(A W^T + b)): exact (erf) GELU in fp32 on the projection
+//                    rounded to the output dtype, then rounded again (F.gelu on an nn.Linear
+//                    output of that dtype);
+//   EPI_ZERO_MASKED  rows whose row_valid entry is 0 are written as zeros after the residual
+//                    add instead of as the residual (the block's trailing masked_fill).
+constexpr int EPI_GELU = 1;
+constexpr int EPI_ZERO_MASKED = 2;
+
+// Exact GELU, x * Phi(x) with Phi(x) = erfc(-x / sqrt 2) / 2, in fp32. erfc comes from the
+// Chebyshev fit of Numerical Recipes (Press et al., "erfcc"; fractional error below 1.2e-7 for
+// every argument):  erfc(z) = t exp(-z^2 - 1.26551223 + t P(t)),  t = 1 / (1 + z / 2),  z >= 0,
+// with erfc(-z) = 2 - erfc(z) for the other sign. Branch-free (one reciprocal, one exponential,
+// twelve FMAs): the epilogue evaluates it on every output of a 256 x 256 tile, where a
+// general-purpose erff with range branches cost ~50% of the GEMM's time.
+MI355_DEVINL float gelu_erf(float x) {
+  const float z = __builtin_fabsf(x) * 0.70710678118654752f;
+  const float t = __builtin_amdgcn_rcpf(__builtin_fmaf(0.5f, z, 1.0f));
+  float p = 0.17087277f;
+  p = __builtin_fmaf(p, t, -0.82215223f);
+  p = __builtin_fmaf(p, t, 1.48851587f);
+  p = __builtin_fmaf(p, t, -1.13520398f);
+  p = __builtin_fmaf(p, t, 0.27886807f);
+  p = __builtin_fmaf(p, t, -0.18628806f);
+  p = __builtin_fmaf(p, t, 0.09678418f);
+  p = __builtin_fmaf(p, t, 0.37409196f);
+  p = __builtin_fmaf(p, t, 1.00002368f);
+  const float arg = __builtin_fmaf(t, p, __builtin_fmaf(-z, z, -1.26551223f));
+  const float half_erfc = 0.5f * t * __builtin_amdgcn_exp2f(arg * 1.4426950408889634f);
+  const float phi = x >= 0.f ? 1.0f - half_erfc : half_erfc;
+  return x * phi;
+}
 
 template <typename TO>
 MI355_DEVINL void store_out(void* C, int64_t idx, float v) {
@@ -395,6 +429,7 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
           } else {
             v[e] = acc[a][b][4 * i4 + e] + bias_n;
           }
+          if (p.epi & EPI_GELU) v[e] = gelu_erf(to_f32(from_f32<TO>(v[e])));
           if (!valid) v[e] = 0.f;
         }
         if constexpr (STAGE_C) {
@@ -411,6 +446,7 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
               if (n >= p.N) continue;
               float y = to_f32(from_f32<TO>(v[e]));  // the projection output, rounded once
               if (p.R) y = y + to_f32(static_cast<const TO*>(p.R)[m * p.ldr + n]);
+              if (!valid && (p.epi & EPI_ZERO_MASKED)) y = 0.f;
               store_out<TO>(p.C, m * p.ldc + n, y);
             }
           }
@@ -449,15 +485,17 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
           u32x4 chunk = *reinterpret_cast<const u32x4*>(cl + r * C_PITCH + c * 16);
           TO* dst = static_cast<TO*>(p.C) + m * p.ldc + n;
           TO* cv = reinterpret_cast<TO*>(&chunk);
+          const bool zero = (p.epi & EPI_ZERO_MASKED) && p.row_valid && p.row_valid[m] == 0;
           if (n + EPC_OUT <= p.N) {
             const TO* rv = reinterpret_cast<const TO*>(&rc[i]);
 #pragma unroll
             for (int e = 0; e < EPC_OUT; ++e) cv[e] = from_f32<TO>(to_f32(cv[e]) + to_f32(rv[e]));
+            if (zero) chunk = u32x4{0u, 0u, 0u, 0u};
             *reinterpret_cast<u32x4*>(dst) = chunk;
           } else {
             const TO* res = Rb + m * p.ldr + n;
             for (int e = 0; e < EPC_OUT && n + e < p.N; ++e)
-              dst[e] = from_f32<TO>(to_f32(cv[e]) + to_f32(res[e]));
+              dst[e] = zero ? from_f32<TO>(0.f) : from_f32<TO>(to_f32(cv[e]) + to_f32(res[e]));
           }
         }
       } else
@@ -467,7 +505,8 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
         if (m >= p.M || n >= p.N) continue;
         u32x4 chunk = *reinterpret_cast<const u32x4*>(cl + r * C_PITCH + c * 16);
         TO* dst = static_cast<TO*>(p.C) + m * p.ldc + n;
-        const TO* res = p.R ? static_cast<const TO*>(p.R) + m * p.ldr + n : nullptr;
+        const bool zero = (p.epi & EPI_ZERO_MASKED) && p.row_valid && p.row_valid[m] == 0;
+        const TO* res = (p.R && !zero) ? static_cast<const TO*>(p.R) + m * p.ldr + n : nullptr;
         if (vec_ok && n + EPC_OUT <= p.N) {
           if (res) {
             // residual add on the rounded projection output (the reference adds two tensors of
@@ -551,9 +590,12 @@ __global__ __launch_bounds__(64 * NWS) void gemm_f32_splitk(GemmArgs p) {
 #pragma unroll
     for (int w = 1; w < NWS; ++w) v += red[w][i][l];
     if (p.bias) v = v + p.bias[n];
-    if (p.row_valid && p.row_valid[m] == 0) v = 0.f;
+    if (p.epi & EPI_GELU) v = gelu_erf(v);
+    const bool masked = p.row_valid && p.row_valid[m] == 0;
+    if (masked) v = 0.f;
     // residual read before the write of the same element: R may be C
     if (p.R) v = v + static_cast<const float*>(p.R)[m * p.ldr + n];
+    if (masked && (p.epi & EPI_ZERO_MASKED)) v = 0.f;
     static_cast<float*>(p.C)[m * p.ldc + n] = v;
   }
 }
@@ -613,7 +655,7 @@ int launch_by_out(const GemmArgs& a, hipStream_t s) {
 namespace {
 int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, const void* W, int64_t ldw,
                    const float* bias, const void* R, int64_t ldr, void* C, int64_t ldc, int64_t M,
-                   int64_t N, int64_t K, const uint8_t* row_valid, void* stream) {
+                   int64_t N, int64_t K, const uint8_t* row_valid, void* stream, int epi = 0) {
   if (M < 0 || N < 0 || K < 0) return MI355_E_BAD_SIZE;
   if (M == 0 || N == 0) return MI355_OK;
   if (!A || !W || !C) return MI355_E_NULL_POINTER;
@@ -640,6 +682,7 @@ int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, cons
   a.N = N;
   a.K = K;
   a.out_dtype = out_dtype;
+  a.epi = epi;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (in_dtype) {
     case MI355_F16: return launch_by_out<_Float16, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
@@ -672,6 +715,24 @@ extern "C" int mi355_gemm_bias_residual(int in_dtype, int out_dtype, const void*
   if (M > 0 && N > 0 && !R) return MI355_E_NULL_POINTER;
   return gemm_bias_impl(in_dtype, out_dtype, A, lda, W, ldw, bias, R, ldr, C, ldc, M, N, K,
                         row_valid, stream);
+}
+
+extern "C" int mi355_gemm_bias_gelu(int in_dtype, int out_dtype, const void* A, int64_t lda,
+                                    const void* W, int64_t ldw, const float* bias, void* C,
+                                    int64_t ldc, int64_t M, int64_t N, int64_t K, void* stream) {
+  return gemm_bias_impl(in_dtype, out_dtype, A, lda, W, ldw, bias, nullptr, 0, C, ldc, M, N, K,
+                        nullptr, stream, EPI_GELU);
+}
+
+extern "C" int mi355_gemm_bias_residual_zero_masked(int in_dtype, int out_dtype, const void* A,
+                                                    int64_t lda, const void* W, int64_t ldw,
+                                                    const float* bias, const void* R, int64_t ldr,
+                                                    void* C, int64_t ldc, int64_t M, int64_t N,
+                                                    int64_t K, const uint8_t* row_valid,
+                                                    void* stream) {
+  if (M > 0 && N > 0 && !R) return MI355_E_NULL_POINTER;
+  return gemm_bias_impl(in_dtype, out_dtype, A, lda, W, ldw, bias, R, ldr, C, ldc, M, N, K,
+                        row_valid, stream, EPI_ZERO_MASKED);
 }
 
 extern "C" int mi355_gemm_i8(const int8_t* A, const int8_t* W, const float* s_a, const float* s_w,

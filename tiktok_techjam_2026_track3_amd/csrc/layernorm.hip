@@ -18,13 +18,19 @@ __global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, i
                                                       const T* __restrict__ gamma,
                                                       const T* __restrict__ beta, float eps,
                                                       T* __restrict__ Y, int64_t ldy, int64_t M,
-                                                      int K) {
+                                                      int K, const uint8_t* __restrict__ row_valid) {
   constexpr int EPV = 16 / static_cast<int>(sizeof(T));  // elements per 16-byte vector
   typedef T tv __attribute__((ext_vector_type(EPV)));
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= M) return;  // whole wave leaves together
   const int nvec = K / EPV;
+  if (row_valid != nullptr && row_valid[row] == 0) {
+    // masked row: zeros (the masked_fill that follows the final norm)
+    T* yr = Y + row * ldy;
+    for (int vi = lane; vi < nvec; vi += 64) *reinterpret_cast<tv*>(yr + static_cast<int64_t>(vi) * EPV) = tv{};
+    return;
+  }
   const T* xr = X + row * ldx;
 
   float xs[NV][EPV];
@@ -77,7 +83,7 @@ __global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, i
 
 template <typename T>
 int launch_ln(const void* X, int64_t ldx, const void* gamma, const void* beta, float eps, void* Y,
-              int64_t ldy, int64_t M, int64_t K, hipStream_t s) {
+              int64_t ldy, int64_t M, int64_t K, const uint8_t* rv, hipStream_t s) {
   constexpr int EPV = 16 / static_cast<int>(sizeof(T));
   const int64_t nvec = K / EPV;
   const int64_t blocks = (M + 3) / 4;
@@ -89,23 +95,23 @@ int launch_ln(const void* X, int64_t ldx, const void* gamma, const void* beta, f
   T* y = static_cast<T*>(Y);
   const int k = static_cast<int>(K);
   if (nvec <= 64)
-    hipLaunchKernelGGL((layernorm_rows<T, 1>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k);
+    hipLaunchKernelGGL((layernorm_rows<T, 1>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   else if (nvec <= 128)
-    hipLaunchKernelGGL((layernorm_rows<T, 2>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k);
+    hipLaunchKernelGGL((layernorm_rows<T, 2>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   else if (nvec <= 256)
-    hipLaunchKernelGGL((layernorm_rows<T, 4>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k);
+    hipLaunchKernelGGL((layernorm_rows<T, 4>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   else if (nvec <= 512)
-    hipLaunchKernelGGL((layernorm_rows<T, 8>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k);
+    hipLaunchKernelGGL((layernorm_rows<T, 8>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   else
-    hipLaunchKernelGGL((layernorm_rows<T, 16>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k);
+    hipLaunchKernelGGL((layernorm_rows<T, 16>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   return static_cast<int>(hipGetLastError());
 }
 
 }  // namespace
 
-extern "C" int mi355_layernorm(int dtype, const void* X, int64_t ldx, const void* gamma,
-                               const void* beta, float eps, void* Y, int64_t ldy, int64_t M,
-                               int64_t K, void* stream) {
+extern "C" int mi355_layernorm_masked(int dtype, const void* X, int64_t ldx, const void* gamma,
+                                      const void* beta, float eps, void* Y, int64_t ldy, int64_t M,
+                                      int64_t K, const uint8_t* row_valid, void* stream) {
   if (M < 0 || K <= 0) return MI355_E_BAD_SIZE;
   if (M == 0) return MI355_OK;
   if (!X || !Y) return MI355_E_NULL_POINTER;
@@ -119,8 +125,14 @@ extern "C" int mi355_layernorm(int dtype, const void* X, int64_t ldx, const void
   if (K / epv > 64 * 16) return MI355_E_UNSUPPORTED;  // row must fit the registers of one wave
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (dtype) {
-    case MI355_F16: return launch_ln<_Float16>(X, ldx, gamma, beta, eps, Y, ldy, M, K, s);
-    case MI355_BF16: return launch_ln<__bf16>(X, ldx, gamma, beta, eps, Y, ldy, M, K, s);
-    default: return launch_ln<float>(X, ldx, gamma, beta, eps, Y, ldy, M, K, s);
+    case MI355_F16: return launch_ln<_Float16>(X, ldx, gamma, beta, eps, Y, ldy, M, K, row_valid, s);
+    case MI355_BF16: return launch_ln<__bf16>(X, ldx, gamma, beta, eps, Y, ldy, M, K, row_valid, s);
+    default: return launch_ln<float>(X, ldx, gamma, beta, eps, Y, ldy, M, K, row_valid, s);
   }
+}
+
+extern "C" int mi355_layernorm(int dtype, const void* X, int64_t ldx, const void* gamma,
+                               const void* beta, float eps, void* Y, int64_t ldy, int64_t M,
+                               int64_t K, void* stream) {
+  return mi355_layernorm_masked(dtype, X, ldx, gamma, beta, eps, Y, ldy, M, K, nullptr, stream);
 }

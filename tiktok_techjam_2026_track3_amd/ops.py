@@ -46,14 +46,18 @@ def _mask_ptr(mask: Optional[torch.Tensor], shape: Tuple[int, ...]) -> int:
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] = None,
            out: Optional[torch.Tensor] = None, row_valid: Optional[torch.Tensor] = None,
            out_dtype: Optional[torch.dtype] = None,
-           residual: Optional[torch.Tensor] = None) -> torch.Tensor:
+           residual: Optional[torch.Tensor] = None, gelu: bool = False,
+           zero_masked_rows: bool = False) -> torch.Tensor:
     """``out[M, N] = x[M, K] @ weight[N, K]^T + bias[N]`` (nn.Linear), fp32 accumulate.
 
     ``x`` may be a row-strided 2-D view (unit column stride); ``weight`` must be contiguous and
     of x's dtype; ``bias`` is fp32. ``out_dtype`` (default x's dtype) may be the other 16-bit
     type for 16-bit inputs. Rows whose ``row_valid`` entry is False are written as zeros.
     With ``residual`` ([M, N] of out_dtype, unit column stride; may be ``out`` itself) the result
-    is ``residual + out_dtype(projection)``, masked rows giving ``residual``.
+    is ``residual + out_dtype(projection)``, masked rows giving ``residual`` -- or zeros with
+    ``zero_masked_rows`` (the block's trailing masked_fill). ``gelu`` applies the exact GELU to
+    the projection rounded to out_dtype (``F.gelu(nn.Linear(...)(x))``); it excludes
+    ``residual`` and ``row_valid``.
     """
     _on_gpu(x, weight, bias, out, row_valid, residual)
     if x.dim() != 2 or weight.dim() != 2:
@@ -75,15 +79,27 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
         out = torch.empty((M, N), device=x.device, dtype=odt)
     elif out.shape != (M, N) or out.dtype != odt or out.stride(1) != 1:
         raise ValueError("out must be [M, N] of out_dtype with unit column stride")
+    if gelu:
+        if residual is not None or row_valid is not None:
+            raise ValueError("the GELU epilogue takes no residual or row mask")
+        st = _lib.lib().mi355_gemm_bias_gelu(
+            _lib.dtype_code(dt), _lib.dtype_code(odt), x.data_ptr(), x.stride(0),
+            weight.data_ptr(), weight.stride(0), bias.data_ptr() if bias is not None else 0,
+            out.data_ptr(), out.stride(0), M, N, K, _stream(x))
+        _lib.check("mi355_gemm_bias_gelu", st)
+        return out
+    if zero_masked_rows and residual is None:
+        raise ValueError("zero_masked_rows is a mode of the residual epilogue")
     if residual is not None:
         if residual.shape != (M, N) or residual.dtype != odt or residual.stride(1) != 1:
             raise ValueError("residual must be [M, N] of out_dtype with unit column stride")
-        st = _lib.lib().mi355_gemm_bias_residual(
+        fn = "mi355_gemm_bias_residual_zero_masked" if zero_masked_rows else "mi355_gemm_bias_residual"
+        st = getattr(_lib.lib(), fn)(
             _lib.dtype_code(dt), _lib.dtype_code(odt), x.data_ptr(), x.stride(0),
             weight.data_ptr(), weight.stride(0), bias.data_ptr() if bias is not None else 0,
             residual.data_ptr(), residual.stride(0), out.data_ptr(), out.stride(0), M, N, K,
             _mask_ptr(row_valid, (M,)), _stream(x))
-        _lib.check("mi355_gemm_bias_residual", st)
+        _lib.check(fn, st)
         return out
     st = _lib.lib().mi355_gemm_bias(
         _lib.dtype_code(dt), _lib.dtype_code(odt), x.data_ptr(), x.stride(0), weight.data_ptr(),
@@ -94,10 +110,12 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
 
 
 def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor],
-               eps: float = 1e-5, out: Optional[torch.Tensor] = None) -> torch.Tensor:
+               eps: float = 1e-5, out: Optional[torch.Tensor] = None,
+               row_valid: Optional[torch.Tensor] = None) -> torch.Tensor:
     """Row LayerNorm of a 2-D ``x`` (nn.LayerNorm over the last dimension): fp32 statistics,
-    output rounded once to x's dtype. ``weight``/``bias`` are contiguous ``[K]`` of x's dtype."""
-    _on_gpu(x, weight, bias, out)
+    output rounded once to x's dtype. ``weight``/``bias`` are contiguous ``[K]`` of x's dtype.
+    Rows whose ``row_valid`` entry is False are written as zeros."""
+    _on_gpu(x, weight, bias, out, row_valid)
     if x.dim() != 2 or x.stride(1) != 1:
         raise ValueError("layer_norm expects a 2-D x with unit column stride")
     M, K = x.shape
@@ -108,6 +126,14 @@ def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[t
         out = torch.empty((M, K), device=x.device, dtype=x.dtype)
     elif out.shape != (M, K) or out.dtype != x.dtype or out.stride(1) != 1:
         raise ValueError("out must be [M, K] of x's dtype with unit column stride")
+    if row_valid is not None:
+        st = _lib.lib().mi355_layernorm_masked(
+            _lib.dtype_code(x.dtype), x.data_ptr(), x.stride(0),
+            weight.data_ptr() if weight is not None else 0,
+            bias.data_ptr() if bias is not None else 0, float(eps), out.data_ptr(), out.stride(0),
+            M, K, _mask_ptr(row_valid, (M,)), _stream(x))
+        _lib.check("mi355_layernorm_masked", st)
+        return out
     st = _lib.lib().mi355_layernorm(
         _lib.dtype_code(x.dtype), x.data_ptr(), x.stride(0),
         weight.data_ptr() if weight is not None else 0, bias.data_ptr() if bias is not None else 0,

@@ -9,6 +9,10 @@
 3. model class   — ``make_user_optimized_transformer(otb)`` returns a subclass of
    ``otb.BaselineTransformer`` that swaps its attention modules on construction, the role of
    ``UserOptimizedTransformer`` (torch_transformer_benchmark.py:175-200).
+
+Each takes a scope: the attention module only (default), ``fuse_block`` (each block's attention
+half -- norm1, attention, residual -- on the kernels, the FFN half left to torch) or
+``full_model`` (every block and the final norm on the kernels, transformer.py).
 """
 from __future__ import annotations
 
@@ -16,6 +20,7 @@ import torch.nn as nn
 import torch.nn.functional as F
 
 from .attention import Int8SelfAttention, SelfAttention
+from .transformer import block_forward, final_norm_forward
 
 _ATTN_ATTRS = ("d_model", "num_heads", "head_dim", "scale", "q_proj", "k_proj", "v_proj", "out_proj")
 
@@ -73,32 +78,90 @@ def swap_blocks(model: nn.Module) -> int:
     return swapped
 
 
-def build(otb, config, int8: bool = False, fuse_block: bool = False) -> nn.Module:
+_FULL_CLASSES: dict = {}
+
+
+def _full_block_class(cls):
+    if cls not in _FULL_CLASSES:
+        _FULL_CLASSES[cls] = type("Kernel" + cls.__name__, (cls,), {"forward": block_forward})
+    return _FULL_CLASSES[cls]
+
+
+def _full_model_forward(self, x, valid_token_mask=None):
+    """BaselineTransformer.forward (torch_transformer_benchmark.py:160-172): the (swapped)
+    blocks, then final_norm + masked_fill as one masked LayerNorm launch."""
+    for layer in self.layers:
+        x = layer(x, valid_token_mask, self.config.causal)
+    return final_norm_forward(self.final_norm, x, valid_token_mask)
+
+
+def swap_model(model: nn.Module) -> int:
+    """Re-class every block of ``model`` so its whole forward runs on the gfx950 kernels
+    (transformer.block_forward) and, when ``model`` has ``layers`` / ``final_norm`` / ``config``,
+    the model itself so the final norm and its row mask do too; returns how many blocks were
+    swapped. Parameters and state-dict keys are untouched."""
+    swapped = 0
+    for mod in list(model.modules()):
+        if all(hasattr(mod, a) for a in _BLOCK_ATTRS) and _is_attention(mod.attention):
+            if not isinstance(mod.attention, SelfAttention) or isinstance(mod.attention, Int8SelfAttention):
+                mod.attention.__class__ = SelfAttention
+                mod.attention.invalidate_caches()
+            base = type(mod)
+            if base in _FUSED_CLASSES.values():
+                base = base.__mro__[1]
+            if base not in _FULL_CLASSES.values():
+                mod.__class__ = _full_block_class(base)
+            swapped += 1
+    if swapped and all(hasattr(model, a) for a in ("layers", "final_norm", "config")):
+        cls = type(model)
+        if not getattr(cls, "_mi355_full_model", False):
+            model.__class__ = type("Kernel" + cls.__name__, (cls,),
+                                   {"forward": _full_model_forward, "_mi355_full_model": True})
+    return swapped
+
+
+def build(otb, config, int8: bool = False, fuse_block: bool = False,
+          full_model: bool = False) -> nn.Module:
     """Plugin contract of the reference harness: a model whose attention runs on gfx950.
 
     ``fuse_block`` also runs each block's attention half (norm1, attention, residual add) as
-    LayerNorm kernel + attention + out projection with the residual fused into its epilogue."""
-    if int8 and fuse_block:
+    LayerNorm kernel + attention + out projection with the residual fused into its epilogue;
+    ``full_model`` runs every block and the final norm on the kernels."""
+    if int8 and (fuse_block or full_model):
         raise ValueError("the fused norm + residual path is built for the 16-bit / fp32 block")
     base = getattr(otb, "UserOptimizedTransformer", None) or otb.BaselineTransformer
     model = base(config)
     if swap_attention(model, int8=int8) == 0:
         raise RuntimeError("no attention module found to replace")
-    if fuse_block and swap_blocks(model) == 0:
+    if full_model:
+        if swap_model(model) == 0:
+            raise RuntimeError("no transformer block found to swap")
+    elif fuse_block and swap_blocks(model) == 0:
         raise RuntimeError("no transformer block found to fuse")
     return model
 
 
-def make_user_optimized_transformer(otb, int8: bool = False, fuse_block: bool = False):
+def make_user_optimized_transformer(otb, int8: bool = False, fuse_block: bool = False,
+                                    full_model: bool = False):
     """A ``UserOptimizedTransformer`` class for the official script module ``otb``."""
-    if int8 and fuse_block:
+    if int8 and (fuse_block or full_model):
         raise ValueError("the fused norm + residual path is built for the 16-bit / fp32 block")
 
     class UserOptimizedTransformer(otb.BaselineTransformer):
         def __init__(self, config):
             super().__init__(config)
             swap_attention(self, int8=int8)
-            if fuse_block:
+            if fuse_block and not full_model:
                 swap_blocks(self)
+            if full_model:
+                for mod in list(self.modules()):
+                    if all(hasattr(mod, a) for a in _BLOCK_ATTRS) and _is_attention(mod.attention):
+                        if type(mod) not in _FULL_CLASSES.values():
+                            mod.__class__ = _full_block_class(type(mod))
+
+        def forward(self, x, valid_token_mask=None):
+            if full_model:
+                return _full_model_forward(self, x, valid_token_mask)
+            return super().forward(x, valid_token_mask)
 
     return UserOptimizedTransformer

@@ -1,0 +1,162 @@
+"""The benchmark's whole transformer on the gfx950 kernels of libmi355attn.so.
+
+``TransformerBlock`` mirrors ``BaselineTransformerBlock`` (torch_transformer_benchmark.py:125-145)
+and ``Transformer`` mirrors ``BaselineTransformer`` / ``UserOptimizedTransformer`` (:148-200):
+same constructor arguments, attribute and parameter names (so a baseline state dict loads with
+``strict=True``) and forward signatures. A block forward is seven launches on the current stream:
+
+  1. LayerNorm kernel                     h = norm1(x)                         (:139)
+  2. packed QKV projection                qkv = h W_qkv^T + b_qkv               (:93-95)
+  3. streamed attention                   ctx                                  (:97-117)
+  4. out projection + residual epilogue   x1 = x + out_proj(ctx), masked rows x (:118-121, :139)
+  5. LayerNorm kernel                     h2 = norm2(x1)                       (:141)
+  6. ffn_in + GELU epilogue               g = gelu(ffn_in(h2))                 (:141)
+  7. ffn_out + residual + row-mask epilogue  y = x1 + ffn_out(g), masked rows 0  (:141-144)
+
+and the model adds one masked LayerNorm launch for ``final_norm`` + masked_fill (:168-171).
+Every rounding point of the reference's dtype arithmetic is kept: each nn.Linear output is
+rounded to the model dtype before GELU / the residual add, and each sum is rounded again.
+fp32, fp16 and bf16 models are supported (bf16 attention cores run in fp16, see
+``SelfAttention.bf16_core_dtype``); the int8 recipe covers the attention projections only and is
+not used here. There is no CPU path: CPU inputs raise.
+"""
+from __future__ import annotations
+
+from typing import Callable, Optional
+
+import torch
+import torch.nn as nn
+
+from . import ops
+from .attention import Int8SelfAttention, SelfAttention
+
+
+def _stamp(*params):
+    return tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in params if p is not None)
+
+
+def _ffn_weights(block: nn.Module, dtype: torch.dtype, device: torch.device):
+    """(W_in [ffn, d], b_in fp32, W_out [d, ffn], b_out fp32) in the model dtype, cached on the
+    block and re-derived when a parameter's storage or version changes."""
+    key = ("ffn", dtype, device, _stamp(block.ffn_in.weight, block.ffn_in.bias,
+                                        block.ffn_out.weight, block.ffn_out.bias))
+    entry = block.__dict__.get("_mi355_ffn")
+    if entry is not None and entry[0] == key:
+        return entry[1]
+    with torch.no_grad():
+        f32 = torch.float32
+
+        def b(lin):
+            if lin.bias is None:
+                return None
+            return lin.bias.to(device=device, dtype=f32).contiguous()
+
+        value = (block.ffn_in.weight.to(device=device, dtype=dtype).contiguous(), b(block.ffn_in),
+                 block.ffn_out.weight.to(device=device, dtype=dtype).contiguous(), b(block.ffn_out))
+    block.__dict__["_mi355_ffn"] = (key, value)
+    return value
+
+
+def _norm_params(norm: nn.LayerNorm, x: torch.Tensor):
+    d = x.shape[-1]
+    if tuple(norm.normalized_shape) != (d,):
+        raise ValueError(f"LayerNorm must normalise the last dimension ({d})")
+    w, b = norm.weight, norm.bias
+    for t in (w, b):
+        if t is not None and (t.dtype != x.dtype or t.device != x.device):
+            raise ValueError("LayerNorm parameters must be on x's device in x's dtype")
+    return (w.detach() if w is not None else None), (b.detach() if b is not None else None)
+
+
+def block_forward(block: nn.Module, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor],
+                  causal: bool, marks: Optional[Callable[[str], None]] = None) -> torch.Tensor:
+    """BaselineTransformerBlock.forward (torch_transformer_benchmark.py:134-145) on the gfx950
+    kernels, for any module with the block's attributes whose ``attention`` is a SelfAttention.
+
+    ``marks(stage)`` is called before each launch ("norm", "qkv", "attn", "out", "norm2",
+    "ffn_in", "ffn_out") and after the last ("end")."""
+    mark = marks or (lambda _stage: None)
+    attn = block.attention
+    if not isinstance(attn, SelfAttention) or isinstance(attn, Int8SelfAttention):
+        raise TypeError("the block's attention must be a (16-bit / fp32) SelfAttention")
+    B, S = attn._check_input(x)
+    d = attn.d_model
+    _, row_valid = attn._resolve_mask(valid_token_mask, B, S, x.device)
+
+    def inner(stage):
+        if stage != "end":
+            mark(stage)
+
+    x1 = attn.forward_residual(x, block.norm1, valid_token_mask, causal, marks=inner)
+    x1 = x1.reshape(B * S, d)
+    w2, b2 = _norm_params(block.norm2, x)
+    w_in, b_in, w_out, b_out = _ffn_weights(block, x.dtype, x.device)
+    mark("norm2")
+    h2 = ops.layer_norm(x1, w2, b2, block.norm2.eps)
+    mark("ffn_in")
+    g = ops.linear(h2, w_in, b_in, gelu=True, out_dtype=x.dtype)
+    mark("ffn_out")
+    y = ops.linear(g, w_out, b_out, residual=x1, row_valid=row_valid, zero_masked_rows=True,
+                   out_dtype=x.dtype)
+    mark("end")
+    return y.view(B, S, d)
+
+
+def final_norm_forward(norm: nn.LayerNorm, x: torch.Tensor,
+                       valid_token_mask: Optional[torch.Tensor]) -> torch.Tensor:
+    """``final_norm(x)`` then ``masked_fill(~valid_token_mask[..., None], 0)``
+    (torch_transformer_benchmark.py:168-171) as one masked LayerNorm launch."""
+    if x.dim() != 3:
+        raise ValueError("expected x of shape [B, S, d]")
+    B, S, d = x.shape
+    if x.device.type != "cuda":
+        raise RuntimeError("the transformer runs only on the GPU kernels (no CPU path)")
+    row_valid = None
+    if valid_token_mask is not None:
+        if valid_token_mask.dtype != torch.bool or tuple(valid_token_mask.shape) != (B, S):
+            raise ValueError(f"valid_token_mask must be a bool tensor of shape ({B}, {S})")
+        row_valid = valid_token_mask.contiguous().view(B * S)
+    w, b = _norm_params(norm, x)
+    x2 = x.reshape(B * S, d)
+    if not x2.is_contiguous():
+        x2 = x2.contiguous()
+    return ops.layer_norm(x2, w, b, norm.eps, row_valid=row_valid).view(B, S, d)
+
+
+class TransformerBlock(nn.Module):
+    """Pre-LN transformer block with the reference's API (torch_transformer_benchmark.py:125-145)."""
+
+    def __init__(self, d_model: int, num_heads: int, ffn_dim: int) -> None:
+        super().__init__()
+        self.norm1 = nn.LayerNorm(d_model)
+        self.attention = SelfAttention(d_model, num_heads)
+        self.norm2 = nn.LayerNorm(d_model)
+        self.ffn_in = nn.Linear(d_model, ffn_dim)
+        self.ffn_out = nn.Linear(ffn_dim, d_model)
+
+    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor],
+                causal: bool) -> torch.Tensor:
+        return block_forward(self, x, valid_token_mask, causal)
+
+
+class Transformer(nn.Module):
+    """``BaselineTransformer`` with the reference's API (torch_transformer_benchmark.py:148-172).
+
+    ``config`` needs ``d_model``, ``num_heads``, ``ffn_dim``, ``num_layers`` and ``causal``
+    (the reference's TransformerConfig, :29-56)."""
+
+    def __init__(self, config) -> None:
+        super().__init__()
+        self.config = config
+        self.layers = nn.ModuleList(
+            [TransformerBlock(config.d_model, config.num_heads, config.ffn_dim)
+             for _ in range(config.num_layers)])
+        self.final_norm = nn.LayerNorm(config.d_model)
+
+    def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        for layer in self.layers:
+            x = layer(x, valid_token_mask, self.config.causal)
+        return final_norm_forward(self.final_norm, x, valid_token_mask)
+
+
+UserOptimizedTransformer = Transformer
