@@ -12,6 +12,9 @@ Contents (each function cites the reference file:line it restates):
   int8.py       numpy restatement of the W8A8 recipe (``_quant_rows``, ``_int8_pack``,
                 ``_int8_linear``) with exact integer GEMM;
   predicate.py  the elementwise ``abs <= atol OR abs <= rtol*|ref|`` comparator;
+  block.py      torch-CPU restatement of the rest of the block and model: exact GELU, the FFN
+                half ``x + ffn_out(gelu(ffn_in(norm2(x))))`` with its row mask, the whole block
+                and the L-layer model with the final norm, and fp64 brute forces;
   model.py      module-level restatement of the benchmark's transformer classes, used as the
                 ``otb`` argument of the plugin contract in tests.
 
@@ -27,5 +30,12 @@ How each function is pinned (the reference ships no golden vectors for this path
   int8.int8_gemm               brute-force int64 loops on small shapes
   int8.int8_linear             hand-computed dequantisation on a 1x1x1 case
   predicate.compare_outputs    hand-built cases for each clause (atol, rtol, NaN, inf)
-All pins live in tests/test_oracle.py.
+  block.gelu                   math.erf fp64 brute force; x * Phi(x) at textbook Phi(1), Phi(2);
+                               gelu(x) - gelu(-x) = x; the tanh approximation and a missing
+                               1/sqrt(2) are caught
+  block.ffn_half               fp64 brute force (per-row LayerNorm, np.dot, math.erf); planted
+                               mistakes (no residual, mask before the residual, no norm) fail
+  block.transformer_block /    equal the module classes of model.py (nn.LayerNorm, nn.Linear,
+  block.transformer            F.gelu) and the composition attention_half -> ffn_half
+Pins live in tests/test_oracle.py and tests/test_oracle_block.py.
 """

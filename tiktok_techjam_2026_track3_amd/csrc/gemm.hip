@@ -47,7 +47,7 @@ struct GemmArgs {
 // Epilogue options beyond bias / row mask / residual:
 //   EPI_GELU         y = gelu(round(A W^T + b)): exact (erf) GELU in fp32 on the projection
 //                    rounded to the output dtype, then rounded again (F.gelu on an nn.Linear
-//                    output of that dtype);
+//                    output of that dtype); selects the GELU instantiation of the kernels;
 //   EPI_ZERO_MASKED  rows whose row_valid entry is 0 are written as zeros after the residual
 //                    add instead of as the residual (the block's trailing masked_fill).
 constexpr int EPI_GELU = 1;
@@ -133,7 +133,7 @@ MI355_DEVINL void tile_coords(int64_t pid, int64_t ntm, int64_t ntn, int64_t& tm
 // M0 + 16*lane), so no registers or ds_write instructions carry the tiles, into a ring of NST
 // slots of CHK chunks per row. Requires K % BK == 0. Otherwise a register-staged, double-
 // buffered loader with bounds checks runs (8 chunks per row).
-template <typename T, typename TO, int BM, int BN, int WM, int WN, bool INT8, bool DIRECT>
+template <typename T, typename TO, int BM, int BN, int WM, int WN, bool INT8, bool DIRECT, bool GELU>
 __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) void gemm_kernel(GemmArgs p) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
@@ -429,7 +429,7 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
           } else {
             v[e] = acc[a][b][4 * i4 + e] + bias_n;
           }
-          if (p.epi & EPI_GELU) v[e] = gelu_erf(to_f32(from_f32<TO>(v[e])));
+          if constexpr (GELU) v[e] = gelu_erf(to_f32(from_f32<TO>(v[e])));
           if (!valid) v[e] = 0.f;
         }
         if constexpr (STAGE_C) {
@@ -540,7 +540,7 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
 // U chunk pairs per wave requested before the first MFMA. The NWS partial tiles are summed
 // through LDS in wave order (deterministic), then bias, row mask and residual are applied per
 // element as in gemm_kernel's epilogue and the tile is written row by row.
-template <int NWS>
+template <int NWS, bool GELU>
 __global__ __launch_bounds__(64 * NWS) void gemm_f32_splitk(GemmArgs p) {
   constexpr int U = 4;
   constexpr int PITCH = 65;  // padded: the reduction reads 32 features of one token per half-wave
@@ -590,7 +590,7 @@ __global__ __launch_bounds__(64 * NWS) void gemm_f32_splitk(GemmArgs p) {
 #pragma unroll
     for (int w = 1; w < NWS; ++w) v += red[w][i][l];
     if (p.bias) v = v + p.bias[n];
-    if (p.epi & EPI_GELU) v = gelu_erf(v);
+    if constexpr (GELU) v = gelu_erf(v);
     const bool masked = p.row_valid && p.row_valid[m] == 0;
     if (masked) v = 0.f;
     // residual read before the write of the same element: R may be C
@@ -604,7 +604,12 @@ int launch_gemm_f32_splitk(const GemmArgs& a, hipStream_t stream) {
   constexpr int NWS = 8;
   const int64_t tiles = ((a.M + 31) / 32) * ((a.N + 31) / 32);
   const dim3 grid(static_cast<unsigned>(tiles)), block(64 * NWS);
-  hipLaunchKernelGGL((gemm_f32_splitk<NWS>), grid, block, 0, stream, a);
+  // GELU is a compile-time variant: as a run-time option its inlined code in the unrolled
+  // epilogue slowed every projection by ~10%
+  if (a.epi & EPI_GELU)
+    hipLaunchKernelGGL((gemm_f32_splitk<NWS, true>), grid, block, 0, stream, a);
+  else
+    hipLaunchKernelGGL((gemm_f32_splitk<NWS, false>), grid, block, 0, stream, a);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -620,10 +625,17 @@ int launch_gemm(const GemmArgs& a, hipStream_t stream) {
   const bool direct = MI355_GEMM_DIRECT && a.K % BK == 0 &&
                       a.lda * static_cast<int64_t>(sizeof(T)) <= (int64_t{1} << 23) &&
                       a.ldw * static_cast<int64_t>(sizeof(T)) <= (int64_t{1} << 23);
-  if (direct)
-    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, true>), grid, block, 0, stream, a);
+  // GELU is a compile-time variant (as a run-time option its inlined code in the unrolled
+  // epilogue slowed every projection by ~10%); the int8 projections never use it
+  const bool gelu = !INT8 && (a.epi & EPI_GELU);
+  if (direct && gelu)
+    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, true, !INT8>), grid, block, 0, stream, a);
+  else if (direct)
+    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, true, false>), grid, block, 0, stream, a);
+  else if (gelu)
+    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, false, !INT8>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, false, false>), grid, block, 0, stream, a);
   return static_cast<int>(hipGetLastError());
 }
 
