@@ -130,8 +130,16 @@ MI355_DEVINL float frag_sum(bf16x8 f, float acc) {
 // Scores are kept in the log2 domain: the Q fragments are multiplied once by c = scale*log2(e)
 // (re-rounded to the input dtype), and each score MFMA chain starts from a block holding -mu, the
 // running (lazy) max, so the MFMA output is already s*c - mu and feeds v_exp_f32 directly.
-#ifndef MI355_ATTN_NSTAGE
-#define MI355_ATTN_NSTAGE 2
+#ifndef MI355_ATTN_NSTAGE64
+#define MI355_ATTN_NSTAGE64 2
+#endif
+#ifndef MI355_ATTN_NSTAGE128
+#define MI355_ATTN_NSTAGE128 2
+#endif
+// K / V loads: 1 = buffer loads with fixed per-lane offsets (see issue_loads), 0 = global loads
+// with per-lane 64-bit addresses and clamped keys
+#ifndef MI355_ATTN_BUFLOAD
+#define MI355_ATTN_BUFLOAD 1
 #endif
 
 template <typename T, int HD, int NW, int QG, int KT, int WPE, bool PRIO, bool PIPE, bool CAUSAL,
@@ -158,7 +166,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   // Without the look-ahead a wave reads one stage while the other is in flight (double
   // buffering); with it a wave may read V of sub-tile j and K of j+1 (two stages), so loads go
   // to the stage two ahead of a 3-stage ring.
-  constexpr int NSTAGE = PIPE ? 3 : MI355_ATTN_NSTAGE;
+  constexpr int NSTAGE = PIPE ? 3 : (HD == 64 ? MI355_ATTN_NSTAGE64 : MI355_ATTN_NSTAGE128);
   __shared__ u32x4 k_lds[NSTAGE][KT][BN * KCH];
   __shared__ u32x4 v_lds[NSTAGE][KT][BN * KCH];
   // key-mask bytes of each sub-tile: a 1-byte LDS-DMA load writes each lane's byte
@@ -205,26 +213,54 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
 
   // global -> LDS slot (s, k) for 64-key sub-tile j, asynchronously (vmcnt). Lane i of a block
   // lands at LDS block base + 16 i, i.e. row i / KCH, physical chunk i % KCH, so it fetches the
-  // logical chunk that the swizzle places there. Keys past the end are clamped to the last key:
-  // their scores are masked, so their probabilities are exactly 0.
+  // logical chunk that the swizzle places there.
+  // Buffer loads (MI355_ATTN_BUFLOAD): K and V of this (batch, head) are raw buffers whose base
+  // moves to the sub-tile's first key and whose range ends at key Sk, so each lane's byte offset
+  // inside a sub-tile is fixed for the whole sweep and rows past the end read as zeros (their
+  // scores are masked, so their probabilities are exactly 0). A load is then one scalar M0 write
+  // and the load itself; computing 64-bit per-lane addresses (with clamped keys) cost ~12
+  // instructions per load, ~15% of the kernel's time at C2.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  constexpr int LPW = (BLK + NW - 1) / NW;  // blocks per wave per sub-tile
+  const int r = lane / KCH, pc = lane % KCH;
+  uint32_t koff[LPW], voff[LPW];
+#pragma unroll
+  for (int i = 0; i < LPW; ++i) {
+    const int row = (wv + i * NW) * RB + r;
+    const int c = pc ^ swz<KCH>(row);
+    koff[i] = static_cast<uint32_t>(row) * kstride + c * 16;
+    voff[i] = static_cast<uint32_t>(row) * vstride + c * 16;
+  }
   auto issue_loads = [&](int j, int s, int k) {
     const int k0 = j * BN;
     if constexpr (KMASK) {
-      // the sub-tile's 64 mask bytes, one per lane, straight into LDS (clamped like the keys;
-      // each lands zero-extended in the dword kv_lds[s][k][lane])
-      if (wave == NW - 1)
+      // the sub-tile's 64 mask bytes, one per lane, straight into LDS (keys past the end
+      // clamped to the last one; each lands zero-extended in the dword kv_lds[s][k][lane])
+      if (wv == NW - 1)
         dma_lds1(kvb + ((k0 + lane < Sk) ? k0 + lane : Sk - 1), lds_addr_of(&kv_lds[s][k][0]));
     }
-    const int r = lane / KCH, pc = lane % KCH;
+#if MI355_ATTN_BUFLOAD
+    const uint64_t krem = static_cast<uint64_t>(Sk - k0) * kstride;
+    const uint64_t vrem = static_cast<uint64_t>(Sk - k0) * vstride;
+    const u32x4 kr = buffer_rsrc(Kb + static_cast<uint64_t>(k0) * kstride,
+                                 krem > 0xffffffffull ? 0xffffffffu : static_cast<uint32_t>(krem));
+    const u32x4 vr = buffer_rsrc(Vb + static_cast<uint64_t>(k0) * vstride,
+                                 vrem > 0xffffffffull ? 0xffffffffu : static_cast<uint32_t>(vrem));
+#endif
 #pragma unroll
-    for (int i = 0; i < (BLK + NW - 1) / NW; ++i) {
-      const int blk = wave + i * NW;
+    for (int i = 0; i < LPW; ++i) {
+      const int blk = wv + i * NW;
       if (NW > BLK && blk >= BLK) break;  // more waves than blocks: the rest idle here
+#if MI355_ATTN_BUFLOAD
+      buffer_dma_lds16(kr, koff[i], 0, lds_addr_of(&k_lds[s][k][blk * 64]));
+      buffer_dma_lds16(vr, voff[i], 0, lds_addr_of(&v_lds[s][k][blk * 64]));
+#else
       const int row = blk * RB + r;
       const int key = (k0 + row < Sk) ? k0 + row : Sk - 1;
       const int c = pc ^ swz<KCH>(row);
       dma_lds16(Kb + static_cast<uint64_t>(key) * kstride + c * 16, lds_addr_of(&k_lds[s][k][blk * 64]));
       dma_lds16(Vb + static_cast<uint64_t>(key) * vstride + c * 16, lds_addr_of(&v_lds[s][k][blk * 64]));
+#endif
     }
   };
 
