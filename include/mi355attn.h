@@ -36,7 +36,7 @@ extern "C" {
 #define MI355_E_BAD_SIZE (-2)       /* a size is negative or exceeds the supported range */
 #define MI355_E_BAD_DTYPE (-3)      /* dtype code not supported by this entry point */
 #define MI355_E_ALIGNMENT (-4)      /* pointer or leading dimension violates 16-byte vector access */
-#define MI355_E_HEAD_DIM (-5)       /* head_dim not in the supported set {64, 128} */
+#define MI355_E_HEAD_DIM (-5)       /* head_dim not in {8, 16, 32, 48, 64, 80, 96, 128, 192, 256} */
 #define MI355_E_UNSUPPORTED (-6)    /* argument combination not supported */
 
 /* Library version, e.g. 100 for 0.1.0. */
@@ -76,7 +76,11 @@ int mi355_gemm_bias(int in_dtype, int out_dtype, const void* A, int64_t lda, con
  * key_valid (nullable) is a [B, S_k] byte mask with batch stride key_valid_sb; keys with 0 are
  * excluded (:105-108). A query row whose keys are all excluded produces NaN, as softmax over an
  * all -inf row does in the reference.
- * Supported: dtype F32, F16, BF16 with head_dim 64 or 128.
+ * Supported: dtype F32, F16, BF16 with head_dim 8, 16, 32, 48, 64, 80, 96, 128, 192 or 256
+ * (the benchmark's official shapes use 8, 32, 64, 128 and 256: Project/shapes.json). F16/BF16
+ * with head_dim 64 or 128 run on the matrix cores; the other 16-bit head dims and every F32
+ * problem run on a vector-ALU kernel with fp32 arithmetic (16-bit probabilities are rounded the
+ * same way).
  */
 int mi355_attn_fwd(int dtype, const void* Q, const void* K, const void* V, void* O, int64_t B,
                    int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim,

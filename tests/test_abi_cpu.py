@@ -113,8 +113,9 @@ def test_attention_argument_validation():
         return h.mi355_attn_fwd(dtype, q, fake, fake, fake, B, 4, S, S, hd, strides, strides,
                                 strides, ost, scale, 0, None, 0, None)
 
-    assert call(hd=96) == codes["MI355_E_HEAD_DIM"]
-    assert call(hd=256) == codes["MI355_E_HEAD_DIM"]
+    assert call(hd=40) == codes["MI355_E_HEAD_DIM"]
+    assert call(hd=512) == codes["MI355_E_HEAD_DIM"]
+    assert call(hd=4) == codes["MI355_E_HEAD_DIM"]
     assert call(dtype=5) == codes["MI355_E_BAD_DTYPE"]
     assert call(q=None) == codes["MI355_E_NULL_POINTER"]
     assert call(q=fake + 8) == codes["MI355_E_ALIGNMENT"]

@@ -184,9 +184,36 @@ def test_attention_fully_masked_batch_gives_nan(gpu, dtype):
 def test_attention_rejects_unsupported_head_dim(gpu):
     ops = _ops()
     from tiktok_techjam_2026_track3_amd._lib import KernelError
-    q = torch.zeros(1, 8, 1, 96, dtype=torch.float16, device=gpu)
+    q = torch.zeros(1, 8, 1, 40, dtype=torch.float16, device=gpu)
     with pytest.raises(KernelError, match="head_dim"):
         ops.attention(q, q, q)
+
+
+# head dims of the vector-ALU kernel: 8 (2 lanes per query), 16-96 (4 lanes), 192 and 256
+# (8 lanes); the benchmark's official shapes use 8, 32 and 256 (Project/shapes.json)
+VALU_HDS = [8, 16, 32, 48, 80, 96, 192, 256]
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("hd", VALU_HDS)
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("S", [1, 37, 300])
+def test_attention_other_head_dims(gpu, dtype, hd, causal, S):
+    _attn_check(gpu, dtype, 2, 2, S, S, hd, causal, seed=hd + S)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("hd", [8, 32, 256])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_other_head_dims_masked_packed(gpu, dtype, hd, causal):
+    B, S = 3, 130
+    g = torch.Generator().manual_seed(hd)
+    mask = torch.rand(B, S, generator=g) > 0.3
+    mask[:, 0] = True
+    mask[1] = torch.arange(S) < 45
+    _attn_check(gpu, dtype, B, 4, S, S, hd, causal, key_valid=mask, seed=41)
+    _attn_check(gpu, dtype, 2, 4, S, S, hd, causal, packed=True, seed=42)
+    _attn_check(gpu, dtype, 1, 2, 70, 400, hd, False, seed=43, qscale=6.0)
 
 
 # --------------------------------------------------------------------------------- int8

@@ -544,15 +544,18 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   }
 }
 
-// fp32 (VALU): four lanes per query, 16 queries per work-group of NWK waves, so the small fp32
-// problems (128 queries x 4 heads) still spread over many CUs. Lane 4*qq + ds holds dimensions
-// 16*j + 4*ds + (0..3) of query qq's row and of its output accumulator; a score is the sum of
-// the four lanes' partial dot products, exchanged inside the quad with two DPP adds (every lane
-// of the quad ends with the same bits). The keys are split into NWK contiguous ranges, one per
-// wave; each wave stages its keys 8 at a time in its own LDS slot (read back as broadcasts)
-// and fetches the next chunk (and its mask bytes) into registers while it computes the current
-// one, so no work-group barrier is needed in the loop. At the end the NWK partial states of a
-// query are merged through LDS: the common max M, l = sum_w l_w 2^((m_w - M) c), and the output.
+// VALU kernel: every fp32 problem, and 16-bit head dims the MFMA kernel does not take. LQ lanes
+// per query (4, or 2 when head_dim is not a multiple of 16) and 64 / LQ queries per work-group of
+// NWK waves, so the small problems (128 queries x 4 heads) still spread over many CUs. Lane
+// LQ*qq + ds holds the 4-element pieces LQ*j + ds (j < NJ) of query qq's row and of its output
+// accumulator, in fp32; a score is the sum of the LQ lanes' partial dot products, exchanged with
+// DPP adds (every lane of the group ends with the same bits). The keys are split into NWK
+// contiguous ranges, one per wave; each wave stages its keys KB at a time in its own LDS slot
+// (as fp32, read back as broadcasts) and fetches the next chunk (and its mask bytes) into
+// registers while it computes the current one, so no work-group barrier is needed in the loop.
+// 16-bit inputs: probabilities are rounded to the input type before P·V and the row sum adds
+// the rounded values, as the MFMA kernel does. At the end the NWK partial states of a query are
+// merged through LDS: the common max M, l = sum_w l_w 2^((m_w - M) c), and the output.
 MI355_DEVINL float quad_sum(float v) {
   // quad_perm [1,0,3,2] then [2,3,0,1]: after both, each lane holds (a0+a1)+(a2+a3) or its
   // commuted form, which is the same value
@@ -560,44 +563,79 @@ MI355_DEVINL float quad_sum(float v) {
   v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, false));
   return v;
 }
+MI355_DEVINL float pair_sum2(float v) {
+  // quad_perm [1,0,3,2]: lanes 2i and 2i+1 both end with a0 + a1 (commuted, same value)
+  return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, false));
+}
 
-template <int HD, bool CAUSAL, bool KMASK, int NWK>
-__global__ __launch_bounds__(64 * NWK) void attn_fwd_f32(AttnArgs p) {
-  constexpr int NJ = HD / 16;           // 16-byte pieces of a row per lane
-  // keys per staged chunk and per softmax block (head_dim 128: 4, which keeps the chunk's K
-  // reads the compiler hoists within the register budget)
-  constexpr int KB = HD == 64 ? 8 : 4;
-  constexpr int CH = KB * HD / 4;       // 16-byte pieces of one chunk's K (or V) rows
-  constexpr int PL = CH / 64;           // pieces per lane
-  static_assert(CH % 64 == 0, "chunk pieces per lane");
+MI355_DEVINL float oct_sum(float v) {
+  // quad sums, then row_half_mirror (lane i <-> 7 - i within each group of 8) adds the other
+  // quad's sum: both quads end with the same value
+  v = quad_sum(v);
+  return v + __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x141, 0xF, 0xF, false));
+}
+
+template <typename T>
+MI355_DEVINL f32x4 load4(const T* ptr) {
+  if constexpr (sizeof(T) == 4) {
+    return *reinterpret_cast<const f32x4*>(ptr);
+  } else {
+    typedef T t4 __attribute__((ext_vector_type(4)));
+    const t4 v = *reinterpret_cast<const t4*>(ptr);
+    return f32x4{to_f32(v[0]), to_f32(v[1]), to_f32(v[2]), to_f32(v[3])};
+  }
+}
+
+constexpr int gcd_c(int a, int b) { return b == 0 ? a : gcd_c(b, a % b); }
+
+template <int HD>
+struct ValuShape {
+  // lanes per query: 2 when head_dim is not a multiple of 16, 8 above 128 (keeps the query and
+  // accumulator pieces within the register budget), else 4
+  static constexpr int LQ = HD % 16 != 0 ? 2 : (HD > 128 && HD % 32 == 0 ? 8 : 4);
+  static constexpr int QT = 64 / LQ;  // queries per work-group
+  static constexpr int RP = HD / 4;   // 4-element pieces per row
+  static constexpr int NJ = RP / LQ;  // pieces per lane
+  // keys per staged chunk: the compiler hoists a chunk's K reads, so fewer keys for wider rows
+  static constexpr int KB = HD <= 8 ? 32 : HD <= 16 ? 16 : HD <= 64 ? 8 : HD <= 128 ? 4 : 2;
+  static constexpr int CH = KB * RP;            // pieces of one chunk's K (or V) rows
+  static constexpr int PL = (CH + 63) / 64;     // pieces per lane (the last step may be partial)
+  static_assert(HD % 8 == 0 && HD >= 8 && HD <= 256 && RP % LQ == 0, "head_dim");
+};
+
+template <typename T, int HD, bool CAUSAL, bool KMASK, int NWK>
+__global__ __launch_bounds__(64 * NWK) void attn_fwd_valu(AttnArgs p) {
+  using SH = ValuShape<HD>;
+  constexpr int LQ = SH::LQ, QT = SH::QT, RP = SH::RP, NJ = SH::NJ, KB = SH::KB, CH = SH::CH,
+                PL = SH::PL;
   // per wave: K and V pieces of one chunk (the loop), reused as the merge buffer (NJ x 64 pieces
   // per wave) after it
   constexpr int SLOT = 2 * CH > NJ * 64 ? 2 * CH : NJ * 64;
   __shared__ f32x4 lds[NWK][SLOT];
   __shared__ float stat[NWK][2][64];
   const int lane = threadIdx.x & 63;
-  const int qq = lane >> 2, ds = lane & 3;
+  const int qq = lane / LQ, ds = lane % LQ;
   const int wave = __builtin_amdgcn_readfirstlane(static_cast<int>(threadIdx.x >> 6));
   int qt;
   int64_t h, b;
   tile_of_block<CAUSAL>(p, qt, h, b);
-  const int q_wg = qt * 16;
+  const int q_wg = qt * QT;
   const int qi = q_wg + qq;
   const int sq = static_cast<int>(p.Sq), sk = static_cast<int>(p.Sk);
-  const float* __restrict__ Qb = static_cast<const float*>(p.q) + b * p.qs0 + h * p.qs2;
-  const float* __restrict__ Kb = static_cast<const float*>(p.k) + b * p.ks0 + h * p.ks2;
-  const float* __restrict__ Vb = static_cast<const float*>(p.v) + b * p.vs0 + h * p.vs2;
+  const T* __restrict__ Qb = static_cast<const T*>(p.q) + b * p.qs0 + h * p.qs2;
+  const T* __restrict__ Kb = static_cast<const T*>(p.k) + b * p.ks0 + h * p.ks2;
+  const T* __restrict__ Vb = static_cast<const T*>(p.v) + b * p.vs0 + h * p.vs2;
   const uint8_t* __restrict__ kvb = KMASK ? p.kv + b * p.kv_sb : nullptr;
 
   f32x4 q[NJ], acc[NJ];
 #pragma unroll
   for (int j = 0; j < NJ; ++j) {
-    q[j] = qi < sq ? *reinterpret_cast<const f32x4*>(Qb + static_cast<int64_t>(qi) * p.qs1 + 16 * j + 4 * ds)
+    q[j] = qi < sq ? load4(Qb + static_cast<int64_t>(qi) * p.qs1 + 4 * (LQ * j + ds))
                    : f32x4{0.f, 0.f, 0.f, 0.f};
     acc[j] = f32x4{0.f, 0.f, 0.f, 0.f};
   }
   float m = NEG_INF, l = 0.f;
-  const int kend = CAUSAL ? __builtin_elementwise_min(q_wg + 16, sk) : sk;
+  const int kend = CAUSAL ? __builtin_elementwise_min(q_wg + QT, sk) : sk;
   const int per = (kend + NWK - 1) / NWK;
   const int kbeg = wave * per;
   const int kstop = __builtin_elementwise_min(kbeg + per, kend);
@@ -612,9 +650,10 @@ __global__ __launch_bounds__(64 * NWK) void attn_fwd_f32(AttnArgs p) {
 #pragma unroll
     for (int t = 0; t < PL; ++t) {
       const int i = lane + 64 * t;
-      const int kc = __builtin_elementwise_min(k0 + i / (HD / 4), kstop - 1), c4 = i % (HD / 4);
-      nk[t] = *reinterpret_cast<const f32x4*>(Kb + static_cast<int64_t>(kc) * p.ks1 + 4 * c4);
-      nv[t] = *reinterpret_cast<const f32x4*>(Vb + static_cast<int64_t>(kc) * p.vs1 + 4 * c4);
+      if (CH % 64 != 0 && i >= CH) continue;
+      const int kc = __builtin_elementwise_min(k0 + i / RP, kstop - 1), c4 = i % RP;
+      nk[t] = load4(Kb + static_cast<int64_t>(kc) * p.ks1 + 4 * c4);
+      nv[t] = load4(Vb + static_cast<int64_t>(kc) * p.vs1 + 4 * c4);
     }
     if constexpr (KMASK) nm = lane < KB ? kvb[__builtin_elementwise_min(k0 + lane, kstop - 1)] : 0;
   };
@@ -622,6 +661,7 @@ __global__ __launch_bounds__(64 * NWK) void attn_fwd_f32(AttnArgs p) {
   auto stage = [&]() {
 #pragma unroll
     for (int t = 0; t < PL; ++t) {
+      if (CH % 64 != 0 && lane + 64 * t >= CH) continue;
       kt[lane + 64 * t] = nk[t];
       vt[lane + 64 * t] = nv[t];
     }
@@ -645,13 +685,14 @@ __global__ __launch_bounds__(64 * NWK) void attn_fwd_f32(AttnArgs p) {
       float a0 = 0.f, a1 = 0.f, a2 = 0.f, a3 = 0.f;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const f32x4 kv = kt[kk * (HD / 4) + 4 * j + ds];
+        const f32x4 kv = kt[kk * RP + LQ * j + ds];
         a0 = __builtin_fmaf(q[j][0], kv[0], a0);
         a1 = __builtin_fmaf(q[j][1], kv[1], a1);
         a2 = __builtin_fmaf(q[j][2], kv[2], a2);
         a3 = __builtin_fmaf(q[j][3], kv[3], a3);
       }
-      const float d0 = quad_sum((a0 + a1) + (a2 + a3));
+      const float part = (a0 + a1) + (a2 + a3);
+      const float d0 = LQ == 8 ? oct_sum(part) : LQ == 4 ? quad_sum(part) : pair_sum2(part);
       const int key = k0 + kk;
       bool ok = key < kstop;
       if (CAUSAL) ok = ok && key <= qi;
@@ -667,11 +708,12 @@ __global__ __launch_bounds__(64 * NWK) void attn_fwd_f32(AttnArgs p) {
     for (int j = 0; j < NJ; ++j) acc[j] *= alpha;
 #pragma unroll
     for (int kk = 0; kk < KB; ++kk) {
-      const float pk = fast_exp2(__builtin_fmaf(s[kk], p.c, -mu));
+      // the probability as P·V sees it: rounded to the input type (exact for fp32)
+      const float pk = to_f32(from_f32<T>(fast_exp2(__builtin_fmaf(s[kk], p.c, -mu))));
       l += pk;
 #pragma unroll
       for (int j = 0; j < NJ; ++j) {
-        const f32x4 vv = vt[kk * (HD / 4) + 4 * j + ds];
+        const f32x4 vv = vt[kk * RP + LQ * j + ds];
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc[j][e] = __builtin_fmaf(pk, vv[e], acc[j][e]);
       }
@@ -682,7 +724,7 @@ __global__ __launch_bounds__(64 * NWK) void attn_fwd_f32(AttnArgs p) {
     if (more) stage();
   }
 
-  // merge the NWK partial states of each query (the quad's four lanes hold the same m and l)
+  // merge the NWK partial states of each query (the LQ lanes of a query hold the same m and l)
   stat[wave][0][lane] = m;
   stat[wave][1][lane] = l;
   __syncthreads();  // also ends every wave's use of its staging slot
@@ -701,16 +743,23 @@ __global__ __launch_bounds__(64 * NWK) void attn_fwd_f32(AttnArgs p) {
   for (int j = 0; j < NJ; ++j) lds[wave][j * 64 + lane] = acc[j] * scale;
   __syncthreads();
   if (qi < sq) {
-    float* Ob = static_cast<float*>(p.o) + b * p.os0 + static_cast<int64_t>(qi) * p.os1 + h * p.os2;
+    T* Ob = static_cast<T*>(p.o) + b * p.os0 + static_cast<int64_t>(qi) * p.os1 + h * p.os2;
     for (int j = wave; j < NJ; j += NWK) {
       f32x4 sum = lds[0][j * 64 + lane];
 #pragma unroll
       for (int w = 1; w < NWK; ++w) sum += lds[w][j * 64 + lane];
       sum *= inv;
-      // the output pointer is 8-byte aligned: two 8-byte stores
-      typedef float f32x2 __attribute__((ext_vector_type(2)));
-      *reinterpret_cast<f32x2*>(Ob + 16 * j + 4 * ds) = f32x2{sum[0], sum[1]};
-      *reinterpret_cast<f32x2*>(Ob + 16 * j + 4 * ds + 2) = f32x2{sum[2], sum[3]};
+      T* dst = Ob + 4 * (LQ * j + ds);
+      if constexpr (sizeof(T) == 4) {
+        // the output pointer is 8-byte aligned: two 8-byte stores
+        typedef float f32x2 __attribute__((ext_vector_type(2)));
+        *reinterpret_cast<f32x2*>(dst) = f32x2{sum[0], sum[1]};
+        *reinterpret_cast<f32x2*>(dst + 2) = f32x2{sum[2], sum[3]};
+      } else {
+        typedef T t4 __attribute__((ext_vector_type(4)));
+        *reinterpret_cast<t4*>(dst) =
+            t4{from_f32<T>(sum[0]), from_f32<T>(sum[1]), from_f32<T>(sum[2]), from_f32<T>(sum[3])};
+      }
     }
   }
 }
@@ -791,11 +840,12 @@ int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
-template <int HD>
-int launch_f32(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
-  constexpr int NWK = 8;  // waves (key ranges) per 16 queries
+template <typename T, int HD>
+int launch_valu(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
+  constexpr int NWK = 8;  // waves (key ranges) per query tile
+  constexpr int QT = ValuShape<HD>::QT;
   AttnArgs a = a0;
-  a.n_qtiles = static_cast<int>((a.Sq + 15) / 16);
+  a.n_qtiles = static_cast<int>((a.Sq + QT - 1) / QT);
   if (static_cast<int64_t>(a.n_qtiles) * 64 * NWK > 0xffffffffLL) return MI355_E_BAD_SIZE;
   dim3 grid(a.n_qtiles, static_cast<unsigned>(a.H), static_cast<unsigned>(a.B));
   const dim3 block(64 * NWK);
@@ -804,13 +854,44 @@ int launch_f32(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
   if (causal && !flat) return MI355_E_BAD_SIZE;
   if (flat) grid = dim3(static_cast<unsigned>(n), 1, 1);
   if (causal) {
-    if (kmask) hipLaunchKernelGGL((attn_fwd_f32<HD, true, true, NWK>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_fwd_f32<HD, true, false, NWK>), grid, block, 0, s, a);
+    if (kmask) hipLaunchKernelGGL((attn_fwd_valu<T, HD, true, true, NWK>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_fwd_valu<T, HD, true, false, NWK>), grid, block, 0, s, a);
   } else {
-    if (kmask) hipLaunchKernelGGL((attn_fwd_f32<HD, false, true, NWK>), grid, block, 0, s, a);
-    else hipLaunchKernelGGL((attn_fwd_f32<HD, false, false, NWK>), grid, block, 0, s, a);
+    if (kmask) hipLaunchKernelGGL((attn_fwd_valu<T, HD, false, true, NWK>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((attn_fwd_valu<T, HD, false, false, NWK>), grid, block, 0, s, a);
   }
   return static_cast<int>(hipGetLastError());
+}
+
+// head dims of the VALU kernel (fp32: all of them; 16-bit: all but 64 and 128, which the MFMA
+// kernel takes)
+template <typename T>
+int dispatch_valu(const AttnArgs& a, int64_t hd, bool causal, bool kmask, hipStream_t s) {
+  switch (hd) {
+    case 8: return launch_valu<T, 8>(a, causal, kmask, s);
+    case 16: return launch_valu<T, 16>(a, causal, kmask, s);
+    case 32: return launch_valu<T, 32>(a, causal, kmask, s);
+    case 48: return launch_valu<T, 48>(a, causal, kmask, s);
+    case 80: return launch_valu<T, 80>(a, causal, kmask, s);
+    case 96: return launch_valu<T, 96>(a, causal, kmask, s);
+    case 192: return launch_valu<T, 192>(a, causal, kmask, s);
+    case 256: return launch_valu<T, 256>(a, causal, kmask, s);
+    default: break;
+  }
+  if constexpr (sizeof(T) == 4) {
+    if (hd == 64) return launch_valu<T, 64>(a, causal, kmask, s);
+    if (hd == 128) return launch_valu<T, 128>(a, causal, kmask, s);
+  }
+  return MI355_E_HEAD_DIM;
+}
+
+bool head_dim_supported(int64_t hd) {
+  switch (hd) {
+    case 8: case 16: case 32: case 48: case 64: case 80: case 96: case 128: case 192: case 256:
+      return true;
+    default:
+      return false;
+  }
 }
 
 }  // namespace
@@ -828,7 +909,7 @@ extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const voi
   if (dtype != MI355_F32 && dtype != MI355_F16 && dtype != MI355_BF16) return MI355_E_BAD_DTYPE;
   if (B > 65535 || H > 65535 || S_q > (int64_t)1 << 30 || S_k > (int64_t)1 << 30)
     return MI355_E_BAD_SIZE;
-  if (head_dim != 64 && head_dim != 128) return MI355_E_HEAD_DIM;
+  if (!head_dim_supported(head_dim)) return MI355_E_HEAD_DIM;
   if (!(scale > 0.f)) return MI355_E_UNSUPPORTED;
   // per-lane K/V offsets inside a 64-key tile are 32-bit byte offsets
   if (k_strides[1] <= 0 || v_strides[1] <= 0 || k_strides[1] > ((int64_t)1 << 24) ||
@@ -865,8 +946,10 @@ extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const voi
   const bool kmask = key_valid != nullptr;
   const bool cz = causal != 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
-  if (dtype == MI355_F32) {
-    return head_dim == 64 ? launch_f32<64>(a, cz, kmask, s) : launch_f32<128>(a, cz, kmask, s);
+  if (dtype == MI355_F32) return dispatch_valu<float>(a, head_dim, cz, kmask, s);
+  if (head_dim != 64 && head_dim != 128) {
+    return dtype == MI355_F16 ? dispatch_valu<_Float16>(a, head_dim, cz, kmask, s)
+                              : dispatch_valu<__bf16>(a, head_dim, cz, kmask, s);
   }
   if (dtype == MI355_F16) {
     return head_dim == 64
