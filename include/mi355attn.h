@@ -113,6 +113,28 @@ int mi355_gemm_i8(const int8_t* A, const int8_t* W, const float* s_a, const floa
                   const float* bias, int out_dtype, void* C, int64_t ldc, int32_t* acc_out,
                   int64_t M, int64_t N, int64_t K, const uint8_t* row_valid, void* stream);
 
+/* epilogue flags of mi355_gemm_i8_epilogue */
+#define MI355_EPI_GELU 1         /* C = gelu(projection), exact (erf) form */
+#define MI355_EPI_ZERO_MASKED 2  /* with R: rows with row_valid[m] == 0 are written as zeros */
+
+/*
+ * mi355_gemm_i8 with the epilogues of the int8 transformer block (block_forward,
+ * Project/kernels/k008_int8_gemm.py:189-234), so that block runs whole on the kernels:
+ *   epi = MI355_EPI_GELU, R = NULL:  C = gelu(y)        `F.gelu(_int8_linear(h2, f1))` (:228-229)
+ *   epi = 0, R given:                C = R + y, rows with row_valid[m] == 0 keep R
+ *                                    (`attn_out.masked_fill(...); x = x + attn_out`, :221-225)
+ *   epi = MI355_EPI_ZERO_MASKED, R:  C = R + y, rows with row_valid[m] == 0 are zero
+ *                                    (`x = x + out; x.masked_fill(...)`, :230-233)
+ * where y = out_dtype(fp32(acc) * (s_a[m] * s_w[n]) + bias[n]) as in mi355_gemm_i8 (masked rows
+ * of y are 0), and GELU / the residual sum are evaluated in fp32 from y and rounded once to
+ * out_dtype. R (nullable) is [M, N] of out_dtype with row stride ldr and may alias C. GELU
+ * with R is rejected (MI355_E_UNSUPPORTED). Otherwise as mi355_gemm_i8 (no acc_out).
+ */
+int mi355_gemm_i8_epilogue(const int8_t* A, const int8_t* W, const float* s_a, const float* s_w,
+                           const float* bias, int out_dtype, void* C, int64_t ldc, const void* R,
+                           int64_t ldr, int64_t M, int64_t N, int64_t K,
+                           const uint8_t* row_valid, int epi, void* stream);
+
 /*
  * Row LayerNorm: Y[m,:] = (X[m,:] - mean) * rstd * gamma + beta over the last dimension (K), with
  * fp32 mean, biased variance and rstd = 1 / sqrt(var + eps), Y rounded once to dtype. Replaces

@@ -79,7 +79,7 @@ def pack_block(params):
 
 
 def int8_self_attention(x, params, num_heads: int, causal: bool = False, rows=None):
-    """The attention half of ``block_forward`` (k008_int8_gemm.py:189-223) on CPU.
+    """The attention half of ``block_forward`` (k008_int8_gemm.py:189-225) on CPU.
 
     x [B, S, d] (fp16 values) -> quantised QKV projection -> fp16 qkv (:197) -> fp32-math
     attention -> context rounded to fp16 (the fp16 attention output, :207) -> quantised out
@@ -102,3 +102,57 @@ def int8_self_attention(x, params, num_heads: int, causal: bool = False, rows=No
     sel = ctx16 if rows is None else ctx16[rows]
     y, _ = int8_linear(sel.float().numpy(), pk["out_w"], pk["out_s"], pk["out_b"])
     return {"qkv16": qkv16, "ctx16": ctx16, "out": torch.from_numpy(y)}
+
+
+def pack_ffn(params):
+    """Quantised FFN weights of one block (``_int8_cache``, k008_int8_gemm.py:174-176):
+    ffn_in [ffn, d] and ffn_out [d, ffn] as [N, K] int8 with per-output-channel scales."""
+    w1, s1 = quant_weight(params["ffn_in.weight"].float().numpy())
+    w2, s2 = quant_weight(params["ffn_out.weight"].float().numpy())
+    return {"f1_w": w1, "f1_s": s1, "f1_b": params["ffn_in.bias"].float().numpy().astype(F32),
+            "f2_w": w2, "f2_s": s2, "f2_b": params["ffn_out.bias"].float().numpy().astype(F32)}
+
+
+def int8_transformer_block(x, params, num_heads: int, valid_token_mask=None, causal: bool = False,
+                           eps: float = 1e-5):
+    """``block_forward`` of k008_int8_gemm.py:189-234 for an fp32 model, on CPU.
+
+    norm1 (fp32, :195) -> int8 QKV -> fp16 qkv (:196-197) -> attention in fp32 math on the fp16
+    qkv with the key mask, context rounded to fp16 (:206-219) -> int8 out projection of the
+    context (:221) -> masked rows of it zeroed (:223-224) -> x + attn_out (:225) -> norm2
+    (:227) -> int8 ffn_in (:228) -> exact GELU in fp32 (:229) -> int8 ffn_out (:230) ->
+    x + out (:231) -> masked rows zeroed (:232-233). ``params`` uses the block's state-dict keys.
+    Returns a dict of the stages (torch fp32 tensors; qkv16/ctx16 fp16), ``out`` [B, S, d].
+    """
+    import torch
+    from .attention import attention_core, layer_norm
+    from .block import gelu
+
+    B, S, d = x.shape
+    T = B * S
+    hd = d // num_heads
+    att = {k[len("attention."):]: v for k, v in params.items() if k.startswith("attention.")}
+    pk = pack_block(att)
+    pf = pack_ffn(params)
+    xf = x.float().reshape(T, d)
+    rows_valid = None if valid_token_mask is None else valid_token_mask.reshape(T, 1)
+    h = layer_norm(xf, params["norm1.weight"].float(), params["norm1.bias"].float(), eps)
+    qkv32, _ = int8_linear(h.numpy(), pk["qkv_w"], pk["qkv_s"], pk["qkv_b"])
+    qkv16 = torch.from_numpy(qkv32.astype(np.float16))
+    q5 = qkv16.float().view(B, S, 3, num_heads, hd)
+    q, k, v = (q5[:, :, i].transpose(1, 2).contiguous() for i in range(3))
+    ctx = attention_core(q, k, v, hd ** -0.5, causal, valid_token_mask)
+    ctx16 = ctx.transpose(1, 2).reshape(T, d).to(torch.float16)
+    attn_out = torch.from_numpy(int8_linear(ctx16.float().numpy(), pk["out_w"], pk["out_s"],
+                                            pk["out_b"])[0])
+    if rows_valid is not None:
+        attn_out = attn_out.masked_fill(~rows_valid, 0)
+    x1 = xf + attn_out
+    h2 = layer_norm(x1, params["norm2.weight"].float(), params["norm2.bias"].float(), eps)
+    hid = gelu(torch.from_numpy(int8_linear(h2.numpy(), pf["f1_w"], pf["f1_s"], pf["f1_b"])[0]))
+    out = torch.from_numpy(int8_linear(hid.numpy(), pf["f2_w"], pf["f2_s"], pf["f2_b"])[0])
+    y = x1 + out
+    if rows_valid is not None:
+        y = y.masked_fill(~rows_valid, 0)
+    return {"h": h, "qkv16": qkv16, "ctx16": ctx16, "x1": x1, "h2": h2, "g": hid,
+            "out": y.view(B, S, d)}

@@ -16,11 +16,13 @@ Bars:
   judged on the kernel's own input, widened by one bf16 unit in the last place of the rounded
   intermediates that enter the output additively.
 """
+import numpy as np
 import pytest
 import torch
 
 from oracle import attention as OA
 from oracle import block as OB
+from oracle import int8 as OI
 from oracle import model as OM
 from oracle.predicate import compare_outputs
 
@@ -345,3 +347,127 @@ def test_block_weight_updates_invalidate_ffn_cache(gpu):
     with torch.inference_mode():
         c = blk(x, None, False)
     assert not torch.equal(b, c)
+
+
+# ---------------------------------------------------------------------- int8 (W8A8) block
+def _round(a, dtype):
+    return torch.from_numpy(np.asarray(a, dtype=np.float32)).to(dtype).float()
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_int8_block_stages(gpu, dtype, causal):
+    """The W8A8 block (block_forward, k008_int8_gemm.py:189-234) on the kernels, judged stage by
+    stage on the kernel's own intermediates: the quantised activations (values and scales), the
+    fp16 QKV, the residual sums x1 = x + out_proj and y = x1 + ffn_out (masked rows keeping x,
+    then zeroed) bit for bit against the recipe's integer arithmetic; the LayerNorms and the
+    attention by the reference's predicate; the GELU epilogue within 1 ulp of the exact GELU of
+    the same dequantised projection."""
+    from tiktok_techjam_2026_track3_amd import Transformer
+    from tiktok_techjam_2026_track3_amd.transformer import block_forward
+    B, S, d, H, F = 2, 200, 256, 4, 512
+    cfg = OM.TransformerConfig(batch_size=B, seq_len=S, d_model=d, num_heads=H, ffn_dim=F,
+                               num_layers=1, causal=causal)
+    torch.manual_seed(4321)
+    baseline = OM.BaselineTransformer(cfg).eval()
+    with torch.no_grad():
+        for name, prm in baseline.named_parameters():
+            if "norm" in name:
+                prm.add_(0.1 * torch.randn_like(prm))
+    model = Transformer(cfg, int8=True)
+    model.load_state_dict(baseline.state_dict(), strict=True)
+    model = model.to(device=gpu, dtype=dtype).eval()
+    blk = model.layers[0]
+    g = torch.Generator().manual_seed(17)
+    x = torch.randn(B, S, d, generator=g).to(dtype)
+    mask = torch.arange(S)[None, :] < torch.tensor([S, 131])[:, None]
+    T = B * S
+    valid = mask.reshape(T)
+    keep = {}
+    print(f"int8 block dtype={dtype} causal={causal}", flush=True)
+    with torch.inference_mode():
+        y = block_forward(blk, x.to(gpu), mask.to(gpu), causal, keep=keep)
+    k = {n: t.cpu() for n, t in keep.items()}
+    p = {n: t.detach().float().cpu() for n, t in blk.state_dict().items()}
+    att = {n[len("attention."):]: t for n, t in p.items() if n.startswith("attention.")}
+    pk, pf = OI.pack_block(att), OI.pack_ffn(p)
+    xf = x.float().reshape(T, d)
+
+    def ln_check(name, inp, w, b):
+        r = compare_outputs(OA.layer_norm(inp, w, b).to(dtype).float(), k[name].float())
+        print(f"  {name}:", r.summary(), flush=True)
+        assert r.passed, r.summary()
+
+    def quant_check(name, vals):
+        q, s = OI.quant_rows(vals.float().numpy())
+        np.testing.assert_array_equal(k[name + "_i8"].numpy(), q)
+        np.testing.assert_array_equal(k[name + "_scale"].numpy(), s)
+        return q, s
+
+    ln_check("h", xf, p["norm1.weight"], p["norm1.bias"])
+    hq, sh = quant_check("h", k["h"])
+    qkv = OI.dequant(OI.int8_gemm(hq, pk["qkv_w"]), sh, pk["qkv_s"], pk["qkv_b"])
+    assert torch.equal(k["qkv"], torch.from_numpy(qkv.astype(np.float16)))
+    hd = d // H
+    q5 = k["qkv"].float().view(B, S, 3, H, hd)
+    q, kk, v = (q5[:, :, i].transpose(1, 2) for i in range(3))
+    ctx = OA.attention_core(q, kk, v, hd ** -0.5, causal, mask).transpose(1, 2).reshape(T, d)
+    r = compare_outputs(ctx, k["ctx"].reshape(T, d))
+    print("  ctx vs fp32-math attention on the same qkv:", r.summary(), flush=True)
+    assert r.passed, r.summary()
+    cq, sc = quant_check("ctx", k["ctx"].reshape(T, d))
+    o = _round(OI.dequant(OI.int8_gemm(cq, pk["out_w"]), sc, pk["out_s"], pk["out_b"]), dtype)
+    x1 = (xf + o).to(dtype).float()
+    x1[~valid] = xf[~valid]
+    assert torch.equal(k["x1"].float(), x1)
+    ln_check("h2", x1, p["norm2.weight"], p["norm2.bias"])
+    h2q, sh2 = quant_check("h2", k["h2"])
+    f = _round(OI.dequant(OI.int8_gemm(h2q, pf["f1_w"]), sh2, pf["f1_s"], pf["f1_b"]), dtype)
+    exact = OB.gelu(f.double())
+    ulp = _ulp(exact.float(), dtype).double()
+    gd = (k["g"].double() - exact).abs()
+    print(f"  gelu: max |d| / ulp {float((gd / ulp).max()):.3f}", flush=True)
+    assert bool((gd <= ulp + 4e-7).all())
+    gq, sg = quant_check("g", k["g"])
+    o2 = _round(OI.dequant(OI.int8_gemm(gq, pf["f2_w"]), sg, pf["f2_s"], pf["f2_b"]), dtype)
+    want = (x1 + o2).to(dtype).float()
+    want[~valid] = 0
+    assert torch.equal(y.reshape(T, d).float().cpu(), want)
+    if dtype == torch.float32:
+        rec = OI.int8_transformer_block(x, p, H, mask, causal)["out"]
+        print("  reported: end to end vs the int8 recipe:", compare_outputs(rec, y.cpu()).summary(),
+              flush=True)
+    flt = OB.transformer_block(x.float(), p, H, mask, causal)
+    print("  reported: end to end vs the unquantised block:", compare_outputs(flt, y.cpu()).summary(),
+          flush=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_int8_plugin_full_model_equals_transformer(gpu, dtype):
+    """build(otb, config, int8=True, full_model=True) is the same computation as
+    Transformer(config, int8=True); with fuse_block=True only the attention half runs on the
+    kernels (Int8SelfAttention.forward_residual) and the FFN stays the reference's."""
+    from tiktok_techjam_2026_track3_amd import Transformer, build
+    cfg = OM.TransformerConfig(batch_size=2, seq_len=96, d_model=128, num_heads=2, ffn_dim=256,
+                               num_layers=2, causal=True)
+    torch.manual_seed(8)
+    base = OM.BaselineTransformer(cfg)
+    full = build(OM, cfg, int8=True, full_model=True)
+    full.load_state_dict(base.state_dict(), strict=True)
+    ours = Transformer(cfg, int8=True)
+    ours.load_state_dict(base.state_dict(), strict=True)
+    fused = build(OM, cfg, int8=True, fuse_block=True)
+    fused.load_state_dict(base.state_dict(), strict=True)
+    full, ours, fused = (m.to(device=gpu, dtype=dtype).eval() for m in (full, ours, fused))
+    x = torch.randn(2, 96, 128, generator=torch.Generator().manual_seed(9)).to(dtype).to(gpu)
+    mask = torch.ones(2, 96, dtype=torch.bool, device=gpu)
+    mask[1, 70:] = False
+    with torch.inference_mode():
+        a, b = full(x, mask), ours(x, mask)
+        assert torch.equal(a, b)
+        l0 = fused.layers[0]
+        x1 = l0.attention.forward_residual(x, l0.norm1, mask, True)
+        assert torch.equal(x1, ours.layers[0].attention.forward_residual(x, ours.layers[0].norm1,
+                                                                          mask, True))
+        out = fused(x, mask)
+    assert torch.isfinite(out).all() and torch.all(out[~mask] == 0)

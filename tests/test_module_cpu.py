@@ -6,7 +6,8 @@ import torch
 
 from oracle import model as OM
 from tiktok_techjam_2026_track3_amd import (BaselineSelfAttention, Int8SelfAttention, SelfAttention,
-                                            build, make_user_optimized_transformer, swap_attention)
+                                            build, make_user_optimized_transformer, swap_attention,
+                                            swap_blocks, swap_model)
 from tiktok_techjam_2026_track3_amd import workloads as W
 
 
@@ -100,12 +101,20 @@ def test_plugin_fuse_block_reclasses_blocks_only():
     assert not res.missing_keys and not res.unexpected_keys
     assert swap_blocks(cand) == 3                             # idempotent: same classes again
     assert len({type(l) for l in cand.layers}) == 1
-    with pytest.raises(ValueError):
-        build(OM, cfg, int8=True, fuse_block=True)
+    # the int8 recipe swaps the same blocks with W8A8 attention (and keeps it on re-swaps)
+    cand8 = build(OM, cfg, int8=True, fuse_block=True)
+    assert all(type(l.attention) is Int8SelfAttention for l in cand8.layers)
+    assert swap_blocks(cand8, int8=True) == 3
+    assert all(type(l.attention) is Int8SelfAttention for l in cand8.layers)
+    full8 = build(OM, cfg, int8=True, full_model=True)
+    assert all(type(l.attention) is Int8SelfAttention for l in full8.layers)
+    assert all(type(l).__name__.startswith("Kernel") for l in full8.layers)
+    assert swap_model(full8) == 3                             # back to the 16-bit / fp32 attention
+    assert all(type(l.attention) is SelfAttention for l in full8.layers)
     # no CPU route: the fused block's forward raises on CPU tensors
     with pytest.raises(Exception):
         cand(torch.randn(2, 8, 16), torch.ones(2, 8, dtype=torch.bool))
-    with pytest.raises(NotImplementedError):
+    with pytest.raises(RuntimeError, match="GPU"):
         Int8SelfAttention(16, 4).forward_residual(torch.randn(1, 8, 16), torch.nn.LayerNorm(16))
 
 

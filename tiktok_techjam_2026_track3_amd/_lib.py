@@ -54,7 +54,15 @@ _SIGNATURES = {
         C.c_int,
         [_P, _P, _P, _P, _P, C.c_int, _P, _I64, _P, _I64, _I64, _I64, _P, _P],
     ),
+    "mi355_gemm_i8_epilogue": (
+        C.c_int,
+        [_P, _P, _P, _P, _P, C.c_int, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, C.c_int, _P],
+    ),
 }
+
+# epilogue flags of mi355_gemm_i8_epilogue (MI355_EPI_*)
+EPI_GELU = 1
+EPI_ZERO_MASKED = 2
 
 EXPORTED = tuple(_SIGNATURES)
 

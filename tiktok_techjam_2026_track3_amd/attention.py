@@ -218,7 +218,7 @@ class SelfAttention(nn.Module):
 class Int8SelfAttention(SelfAttention):
     """W8A8 variant: int8 projections with exact int32 accumulation, fp16 SDPA.
 
-    Mirrors the attention half of ``block_forward`` in Project/kernels/k008_int8_gemm.py:189-223:
+    Mirrors the attention half of ``block_forward`` in Project/kernels/k008_int8_gemm.py:189-225:
     qkv = fp16(int8_linear(x)) -> fp16 attention -> int8_linear(ctx). The output dtype is the
     input dtype.
     """
@@ -266,6 +266,47 @@ class Int8SelfAttention(SelfAttention):
             keep.update(qkv=qkv, ctx=ctx, x_i8=xq, x_scale=sx, ctx_i8=cq, ctx_scale=sc)
         return out.view(B, S, d)
 
-    def forward_residual(self, *args, **kwargs):
-        raise NotImplementedError("the fused norm + residual path is built for the 16-bit / fp32 "
-                                  "block; the int8 block's attention runs through run()")
+    def forward_residual(self, x: torch.Tensor, norm: nn.LayerNorm,
+                         valid_token_mask: Optional[torch.Tensor] = None, causal: bool = False,
+                         marks: Optional[Callable[[str], None]] = None,
+                         keep: Optional[dict] = None) -> torch.Tensor:
+        """The attention half of the int8 block (block_forward,
+        Project/kernels/k008_int8_gemm.py:189-225): h = norm1(x) (LayerNorm kernel), W8A8 QKV to
+        fp16, fp16 attention, W8A8 out projection with ``x + attn_out`` fused into its epilogue
+        (masked rows keep x, :221-225). ``marks`` as for ``run`` with an extra "norm" stage;
+        ``keep`` (a dict) receives the intermediates."""
+        mark = marks or (lambda _stage: None)
+        B, S = self._check_input(x)
+        d = self.d_model
+        if d % 16:
+            raise ValueError("the int8 path needs d_model % 16 == 0")
+        if tuple(norm.normalized_shape) != (d,):
+            raise ValueError(f"norm must normalise the last dimension ({d})")
+        w_n, b_n = norm.weight, norm.bias
+        for t in (w_n, b_n):
+            if t is not None and (t.dtype != x.dtype or t.device != x.device):
+                raise ValueError("norm parameters must be on x's device in x's dtype")
+        key_valid, row_valid = self._resolve_mask(valid_token_mask, B, S, x.device)
+        wq, s_qkv, b_qkv, wo, s_o, b_o = self._int8_weights(x.device)
+        x2 = x.reshape(B * S, d)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
+        mark("norm")
+        h = ops.layer_norm(x2, w_n.detach() if w_n is not None else None,
+                           b_n.detach() if b_n is not None else None, norm.eps)
+        mark("quant_x")
+        hq, sh = ops.quant_rows_i8(h, mode=0)
+        mark("qkv")
+        qkv = ops.linear_i8(hq, wq, sh, s_qkv, b_qkv, out_dtype=torch.float16)
+        q, k, v = self._qkv_views(qkv, B, S)
+        mark("attn")
+        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid)
+        mark("quant_ctx")
+        cq, sc = ops.quant_rows_i8(ctx.view(B * S, d), mode=0)
+        mark("out")
+        out = ops.linear_i8(cq, wo, sc, s_o, b_o, out_dtype=x.dtype, row_valid=row_valid,
+                            residual=x2)
+        mark("end")
+        if keep is not None:
+            keep.update(h=h, h_i8=hq, h_scale=sh, qkv=qkv, ctx=ctx, ctx_i8=cq, ctx_scale=sc)
+        return out.view(B, S, d)

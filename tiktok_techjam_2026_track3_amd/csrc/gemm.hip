@@ -626,14 +626,14 @@ int launch_gemm(const GemmArgs& a, hipStream_t stream) {
                       a.lda * static_cast<int64_t>(sizeof(T)) <= (int64_t{1} << 23) &&
                       a.ldw * static_cast<int64_t>(sizeof(T)) <= (int64_t{1} << 23);
   // GELU is a compile-time variant (as a run-time option its inlined code in the unrolled
-  // epilogue slowed every projection by ~10%); the int8 projections never use it
-  const bool gelu = !INT8 && (a.epi & EPI_GELU);
+  // epilogue slowed every projection by ~10%)
+  const bool gelu = (a.epi & EPI_GELU) != 0;
   if (direct && gelu)
-    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, true, !INT8>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, true, true>), grid, block, 0, stream, a);
   else if (direct)
     hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, true, false>), grid, block, 0, stream, a);
   else if (gelu)
-    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, false, !INT8>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, false, true>), grid, block, 0, stream, a);
   else
     hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, false, false>), grid, block, 0, stream, a);
   return static_cast<int>(hipGetLastError());
@@ -775,5 +775,41 @@ extern "C" int mi355_gemm_i8(const int8_t* A, const int8_t* W, const float* s_a,
   a.N = N;
   a.K = K;
   a.out_dtype = out_dtype;
+  return launch_by_out<int8_t, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, true>(a, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int mi355_gemm_i8_epilogue(const int8_t* A, const int8_t* W, const float* s_a,
+                                      const float* s_w, const float* bias, int out_dtype, void* C,
+                                      int64_t ldc, const void* R, int64_t ldr, int64_t M,
+                                      int64_t N, int64_t K, const uint8_t* row_valid, int epi,
+                                      void* stream) {
+  if (M < 0 || N < 0 || K < 0) return MI355_E_BAD_SIZE;
+  if (M == 0 || N == 0) return MI355_OK;
+  if (!A || !W || !C || !s_a || !s_w) return MI355_E_NULL_POINTER;
+  if (out_dtype != MI355_F32 && out_dtype != MI355_F16 && out_dtype != MI355_BF16)
+    return MI355_E_BAD_DTYPE;
+  if (epi & ~(MI355_EPI_GELU | MI355_EPI_ZERO_MASKED)) return MI355_E_UNSUPPORTED;
+  // GELU feeds an FFN's hidden layer; a residual follows only an output projection
+  if ((epi & MI355_EPI_GELU) && R) return MI355_E_UNSUPPORTED;
+  if (K % 16 || !aligned16(A) || !aligned16(W)) return MI355_E_ALIGNMENT;
+  if (ldc < N || (R && ldr < N)) return MI355_E_BAD_SIZE;
+  GemmArgs a{};
+  a.A = A;
+  a.W = W;
+  a.bias = bias;
+  a.C = C;
+  a.R = R;
+  a.s_a = s_a;
+  a.s_w = s_w;
+  a.row_valid = row_valid;
+  a.lda = K;
+  a.ldw = K;
+  a.ldc = ldc;
+  a.ldr = ldr;
+  a.M = M;
+  a.N = N;
+  a.K = K;
+  a.out_dtype = out_dtype;
+  a.epi = (epi & MI355_EPI_GELU ? EPI_GELU : 0) | (epi & MI355_EPI_ZERO_MASKED ? EPI_ZERO_MASKED : 0);
   return launch_by_out<int8_t, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, true>(a, static_cast<hipStream_t>(stream));
 }

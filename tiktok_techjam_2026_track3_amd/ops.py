@@ -206,13 +206,19 @@ def quant_rows_i8(x: torch.Tensor, mode: int = 0) -> Tuple[torch.Tensor, torch.T
 def linear_i8(a: torch.Tensor, w: torch.Tensor, s_a: torch.Tensor, s_w: torch.Tensor,
               bias: Optional[torch.Tensor] = None, out_dtype: torch.dtype = torch.float16,
               out: Optional[torch.Tensor] = None, acc_out: Optional[torch.Tensor] = None,
-              row_valid: Optional[torch.Tensor] = None, want_out: bool = True) -> Optional[torch.Tensor]:
-    """W8A8 projection: ``out = fp32(a @ w^T) * (s_a[:, None] * s_w[None, :]) + bias``.
+              row_valid: Optional[torch.Tensor] = None, want_out: bool = True,
+              residual: Optional[torch.Tensor] = None, gelu: bool = False,
+              zero_masked_rows: bool = False) -> Optional[torch.Tensor]:
+    """W8A8 projection: ``y = fp32(a @ w^T) * (s_a[:, None] * s_w[None, :]) + bias``.
 
     ``a`` is ``[M, K]`` int8, ``w`` is ``[N, K]`` int8 (K-major), scales fp32. ``acc_out``
-    (``[M, N]`` int32) receives the raw int32 accumulators when given.
+    (``[M, N]`` int32) receives the raw int32 accumulators when given. Epilogues of the int8
+    transformer block (k008_int8_gemm.py:221-233), each computed in fp32 from y rounded to
+    ``out_dtype`` and rounded once: ``gelu`` gives gelu(y); ``residual`` ([M, N] of out_dtype,
+    may be ``out``) gives residual + y with masked rows keeping the residual, or zeroed with
+    ``zero_masked_rows``. The epilogues do not combine with ``acc_out``.
     """
-    _on_gpu(a, w, s_a, s_w, bias, out, acc_out, row_valid)
+    _on_gpu(a, w, s_a, s_w, bias, out, acc_out, row_valid, residual)
     if a.dtype != torch.int8 or w.dtype != torch.int8:
         raise TypeError("a and w must be int8")
     if not a.is_contiguous() or not w.is_contiguous():
@@ -228,15 +234,36 @@ def linear_i8(a: torch.Tensor, w: torch.Tensor, s_a: torch.Tensor, s_w: torch.Te
     if acc_out is not None and (acc_out.shape != (M, N) or acc_out.dtype != torch.int32
                                 or not acc_out.is_contiguous()):
         raise ValueError("acc_out must be a contiguous int32 [M, N] tensor")
-    if want_out and out is None:
+    epilogue = gelu or residual is not None or zero_masked_rows
+    if epilogue and acc_out is not None:
+        raise ValueError("acc_out does not combine with the gelu / residual epilogues")
+    if zero_masked_rows and residual is None:
+        raise ValueError("zero_masked_rows needs a residual")
+    if gelu and residual is not None:
+        raise ValueError("gelu does not combine with a residual")
+    if residual is not None and (residual.shape != (M, N) or residual.dtype != out_dtype
+                                 or residual.stride(1) != 1):
+        raise ValueError("residual must be [M, N] of out_dtype with unit column stride")
+    if (want_out or epilogue) and out is None:
         out = torch.empty((M, N), device=a.device, dtype=out_dtype)
     if out is not None and (out.shape != (M, N) or out.dtype != out_dtype or out.stride(1) != 1):
         raise ValueError("out must be [M, N] of out_dtype with unit column stride")
+    mask = _mask_ptr(row_valid, (M,))
+    if epilogue:
+        flags = (_lib.EPI_GELU if gelu else 0) | (_lib.EPI_ZERO_MASKED if zero_masked_rows else 0)
+        st = _lib.lib().mi355_gemm_i8_epilogue(
+            a.data_ptr(), w.data_ptr(), s_a.data_ptr(), s_w.data_ptr(),
+            bias.data_ptr() if bias is not None else 0, _lib.dtype_code(out_dtype),
+            out.data_ptr(), out.stride(0),
+            residual.data_ptr() if residual is not None else 0,
+            residual.stride(0) if residual is not None else N, M, N, K, mask, flags, _stream(a))
+        _lib.check("mi355_gemm_i8_epilogue", st)
+        return out
     st = _lib.lib().mi355_gemm_i8(
         a.data_ptr(), w.data_ptr(), s_a.data_ptr(), s_w.data_ptr(),
         bias.data_ptr() if bias is not None else 0, _lib.dtype_code(out_dtype),
         out.data_ptr() if out is not None else 0, out.stride(0) if out is not None else N,
         acc_out.data_ptr() if acc_out is not None else 0, M, N, K,
-        _mask_ptr(row_valid, (M,)), _stream(a))
+        mask, _stream(a))
     _lib.check("mi355_gemm_i8", st)
     return out

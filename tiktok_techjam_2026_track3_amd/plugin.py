@@ -62,16 +62,22 @@ def _fused_class(cls):
     return _FUSED_CLASSES[cls]
 
 
-def swap_blocks(model: nn.Module) -> int:
+def _set_attention_class(mod: nn.Module, int8: bool) -> None:
+    cls = Int8SelfAttention if int8 else SelfAttention
+    if type(mod.attention) is not cls:
+        mod.attention.__class__ = cls
+        mod.attention.invalidate_caches()
+
+
+def swap_blocks(model: nn.Module, int8: bool = False) -> int:
     """Re-class every transformer block of ``model`` (modules with norm1 / attention / norm2 /
-    ffn_in / ffn_out) so its attention half runs fused, and its attention on gfx950; returns how
-    many blocks were swapped. Parameters and state-dict keys are untouched."""
+    ffn_in / ffn_out) so its attention half runs fused, and its attention on gfx950 (the W8A8
+    attention of k008_int8_gemm.py:189-225 with ``int8``); returns how many blocks were swapped.
+    Parameters and state-dict keys are untouched."""
     swapped = 0
     for mod in list(model.modules()):
         if all(hasattr(mod, a) for a in _BLOCK_ATTRS) and _is_attention(mod.attention):
-            if not isinstance(mod.attention, SelfAttention) or isinstance(mod.attention, Int8SelfAttention):
-                mod.attention.__class__ = SelfAttention
-                mod.attention.invalidate_caches()
+            _set_attention_class(mod, int8)
             if type(mod) not in _FUSED_CLASSES.values():
                 mod.__class__ = _fused_class(type(mod))
             swapped += 1
@@ -95,17 +101,16 @@ def _full_model_forward(self, x, valid_token_mask=None):
     return final_norm_forward(self.final_norm, x, valid_token_mask)
 
 
-def swap_model(model: nn.Module) -> int:
+def swap_model(model: nn.Module, int8: bool = False) -> int:
     """Re-class every block of ``model`` so its whole forward runs on the gfx950 kernels
-    (transformer.block_forward) and, when ``model`` has ``layers`` / ``final_norm`` / ``config``,
-    the model itself so the final norm and its row mask do too; returns how many blocks were
-    swapped. Parameters and state-dict keys are untouched."""
+    (transformer.block_forward; with ``int8`` the W8A8 block of k008_int8_gemm.py:189-234) and,
+    when ``model`` has ``layers`` / ``final_norm`` / ``config``, the model itself so the final
+    norm and its row mask do too; returns how many blocks were swapped. Parameters and
+    state-dict keys are untouched."""
     swapped = 0
     for mod in list(model.modules()):
         if all(hasattr(mod, a) for a in _BLOCK_ATTRS) and _is_attention(mod.attention):
-            if not isinstance(mod.attention, SelfAttention) or isinstance(mod.attention, Int8SelfAttention):
-                mod.attention.__class__ = SelfAttention
-                mod.attention.invalidate_caches()
+            _set_attention_class(mod, int8)
             base = type(mod)
             if base in _FUSED_CLASSES.values():
                 base = base.__mro__[1]
@@ -126,17 +131,16 @@ def build(otb, config, int8: bool = False, fuse_block: bool = False,
 
     ``fuse_block`` also runs each block's attention half (norm1, attention, residual add) as
     LayerNorm kernel + attention + out projection with the residual fused into its epilogue;
-    ``full_model`` runs every block and the final norm on the kernels."""
-    if int8 and (fuse_block or full_model):
-        raise ValueError("the fused norm + residual path is built for the 16-bit / fp32 block")
+    ``full_model`` runs every block and the final norm on the kernels. ``int8`` selects the W8A8
+    recipe of k008_int8_gemm.py (attention projections; with ``full_model`` the FFN too)."""
     base = getattr(otb, "UserOptimizedTransformer", None) or otb.BaselineTransformer
     model = base(config)
     if swap_attention(model, int8=int8) == 0:
         raise RuntimeError("no attention module found to replace")
     if full_model:
-        if swap_model(model) == 0:
+        if swap_model(model, int8=int8) == 0:
             raise RuntimeError("no transformer block found to swap")
-    elif fuse_block and swap_blocks(model) == 0:
+    elif fuse_block and swap_blocks(model, int8=int8) == 0:
         raise RuntimeError("no transformer block found to fuse")
     return model
 
@@ -144,15 +148,13 @@ def build(otb, config, int8: bool = False, fuse_block: bool = False,
 def make_user_optimized_transformer(otb, int8: bool = False, fuse_block: bool = False,
                                     full_model: bool = False):
     """A ``UserOptimizedTransformer`` class for the official script module ``otb``."""
-    if int8 and (fuse_block or full_model):
-        raise ValueError("the fused norm + residual path is built for the 16-bit / fp32 block")
 
     class UserOptimizedTransformer(otb.BaselineTransformer):
         def __init__(self, config):
             super().__init__(config)
             swap_attention(self, int8=int8)
             if fuse_block and not full_model:
-                swap_blocks(self)
+                swap_blocks(self, int8=int8)
             if full_model:
                 for mod in list(self.modules()):
                     if all(hasattr(mod, a) for a in _BLOCK_ATTRS) and _is_attention(mod.attention):

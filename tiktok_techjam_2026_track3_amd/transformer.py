@@ -17,8 +17,11 @@ and the model adds one masked LayerNorm launch for ``final_norm`` + masked_fill 
 Every rounding point of the reference's dtype arithmetic is kept: each nn.Linear output is
 rounded to the model dtype before GELU / the residual add, and each sum is rounded again.
 fp32, fp16 and bf16 models are supported (bf16 attention cores run in fp16, see
-``SelfAttention.bf16_core_dtype``); the int8 recipe covers the attention projections only and is
-not used here. There is no CPU path: CPU inputs raise.
+``SelfAttention.bf16_core_dtype``). A block whose attention is an ``Int8SelfAttention`` runs the
+int8 block of Project/kernels/k008_int8_gemm.py:189-234 instead: all four projections W8A8
+(per-token activation scales from the quantisation kernel, per-channel weight scales), each
+projection input quantised by one extra launch, GELU and both residual adds fused into the int8
+GEMM epilogues. There is no CPU path: CPU inputs raise.
 """
 from __future__ import annotations
 
@@ -57,6 +60,29 @@ def _ffn_weights(block: nn.Module, dtype: torch.dtype, device: torch.device):
     return value
 
 
+def _ffn_weights_i8(block: nn.Module, device: torch.device):
+    """(W_in int8 [ffn, d], s_in, b_in, W_out int8 [d, ffn], s_out, b_out): the weight recipe of
+    ``_int8_pack`` (k008_int8_gemm.py:154-158) applied by the quantisation kernel to the fp32
+    weights, cached on the block like ``_ffn_weights``."""
+    key = ("ffn_i8", device, _stamp(block.ffn_in.weight, block.ffn_in.bias,
+                                    block.ffn_out.weight, block.ffn_out.bias))
+    entry = block.__dict__.get("_mi355_ffn_i8")
+    if entry is not None and entry[0] == key:
+        return entry[1]
+    with torch.no_grad():
+        f32 = torch.float32
+
+        def pack(lin):
+            w = lin.weight.to(device=device, dtype=f32).contiguous()
+            w_i8, s_w = ops.quant_rows_i8(w, mode=1)
+            b = None if lin.bias is None else lin.bias.to(device=device, dtype=f32).contiguous()
+            return w_i8, s_w, b
+
+        value = pack(block.ffn_in) + pack(block.ffn_out)
+    block.__dict__["_mi355_ffn_i8"] = (key, value)
+    return value
+
+
 def _norm_params(norm: nn.LayerNorm, x: torch.Tensor):
     d = x.shape[-1]
     if tuple(norm.normalized_shape) != (d,):
@@ -69,16 +95,21 @@ def _norm_params(norm: nn.LayerNorm, x: torch.Tensor):
 
 
 def block_forward(block: nn.Module, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor],
-                  causal: bool, marks: Optional[Callable[[str], None]] = None) -> torch.Tensor:
+                  causal: bool, marks: Optional[Callable[[str], None]] = None,
+                  keep: Optional[dict] = None) -> torch.Tensor:
     """BaselineTransformerBlock.forward (torch_transformer_benchmark.py:134-145) on the gfx950
-    kernels, for any module with the block's attributes whose ``attention`` is a SelfAttention.
+    kernels, for any module with the block's attributes whose ``attention`` is a SelfAttention
+    (or an Int8SelfAttention: the W8A8 block).
 
     ``marks(stage)`` is called before each launch ("norm", "qkv", "attn", "out", "norm2",
-    "ffn_in", "ffn_out") and after the last ("end")."""
+    "ffn_in", "ffn_out"; the int8 block adds its quantisation launches) and after the last
+    ("end"). ``keep`` (a dict) receives the int8 block's intermediates."""
     mark = marks or (lambda _stage: None)
     attn = block.attention
-    if not isinstance(attn, SelfAttention) or isinstance(attn, Int8SelfAttention):
-        raise TypeError("the block's attention must be a (16-bit / fp32) SelfAttention")
+    if not isinstance(attn, SelfAttention):
+        raise TypeError("the block's attention must be a SelfAttention or Int8SelfAttention")
+    if isinstance(attn, Int8SelfAttention):
+        return _block_forward_i8(block, x, valid_token_mask, causal, mark, keep)
     B, S = attn._check_input(x)
     d = attn.d_model
     _, row_valid = attn._resolve_mask(valid_token_mask, B, S, x.device)
@@ -99,6 +130,50 @@ def block_forward(block: nn.Module, x: torch.Tensor, valid_token_mask: Optional[
     y = ops.linear(g, w_out, b_out, residual=x1, row_valid=row_valid, zero_masked_rows=True,
                    out_dtype=x.dtype)
     mark("end")
+    return y.view(B, S, d)
+
+
+def _block_forward_i8(block: nn.Module, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor],
+                      causal: bool, mark: Callable[[str], None],
+                      keep: Optional[dict] = None) -> torch.Tensor:
+    """The int8 block (block_forward, Project/kernels/k008_int8_gemm.py:189-234): the attention
+    half from Int8SelfAttention.forward_residual, then h2 = norm2(x1), g = gelu(int8_linear(h2))
+    (:227-229) and y = x1 + int8_linear(g) with masked rows zeroed (:230-233). Every projection
+    input is quantised per row by the quantisation kernel (``_quant_rows``, :148-151) from its
+    values in x's dtype (fp32 for the benchmark's default models, as in the reference)."""
+    attn = block.attention
+    B, S = attn._check_input(x)
+    d = attn.d_model
+    ffn = block.ffn_in.out_features
+    if ffn % 16:
+        raise ValueError("the int8 FFN needs ffn_dim % 16 == 0")
+    _, row_valid = attn._resolve_mask(valid_token_mask, B, S, x.device)
+
+    def inner(stage):
+        if stage != "end":
+            mark(stage)
+
+    attn_keep = {} if keep is not None else None
+    x1 = attn.forward_residual(x, block.norm1, valid_token_mask, causal, marks=inner,
+                               keep=attn_keep)
+    x1 = x1.reshape(B * S, d)
+    w2, b2 = _norm_params(block.norm2, x)
+    w_in, s_in, b_in, w_out, s_out, b_out = _ffn_weights_i8(block, x.device)
+    mark("norm2")
+    h2 = ops.layer_norm(x1, w2, b2, block.norm2.eps)
+    mark("quant_h2")
+    hq, sh = ops.quant_rows_i8(h2, mode=0)
+    mark("ffn_in")
+    g = ops.linear_i8(hq, w_in, sh, s_in, b_in, out_dtype=x.dtype, gelu=True)
+    mark("quant_g")
+    gq, sg = ops.quant_rows_i8(g, mode=0)
+    mark("ffn_out")
+    y = ops.linear_i8(gq, w_out, sg, s_out, b_out, out_dtype=x.dtype, residual=x1,
+                      row_valid=row_valid, zero_masked_rows=True)
+    mark("end")
+    if keep is not None:
+        keep.update(attn_keep)
+        keep.update(x1=x1, h2=h2, h2_i8=hq, h2_scale=sh, g=g, g_i8=gq, g_scale=sg)
     return y.view(B, S, d)
 
 
@@ -126,10 +201,10 @@ def final_norm_forward(norm: nn.LayerNorm, x: torch.Tensor,
 class TransformerBlock(nn.Module):
     """Pre-LN transformer block with the reference's API (torch_transformer_benchmark.py:125-145)."""
 
-    def __init__(self, d_model: int, num_heads: int, ffn_dim: int) -> None:
+    def __init__(self, d_model: int, num_heads: int, ffn_dim: int, int8: bool = False) -> None:
         super().__init__()
         self.norm1 = nn.LayerNorm(d_model)
-        self.attention = SelfAttention(d_model, num_heads)
+        self.attention = (Int8SelfAttention if int8 else SelfAttention)(d_model, num_heads)
         self.norm2 = nn.LayerNorm(d_model)
         self.ffn_in = nn.Linear(d_model, ffn_dim)
         self.ffn_out = nn.Linear(ffn_dim, d_model)
@@ -143,13 +218,14 @@ class Transformer(nn.Module):
     """``BaselineTransformer`` with the reference's API (torch_transformer_benchmark.py:148-172).
 
     ``config`` needs ``d_model``, ``num_heads``, ``ffn_dim``, ``num_layers`` and ``causal``
-    (the reference's TransformerConfig, :29-56)."""
+    (the reference's TransformerConfig, :29-56). ``int8`` builds the W8A8 blocks of
+    Project/kernels/k008_int8_gemm.py:189-234 (same parameters; the int8 weights are derived)."""
 
-    def __init__(self, config) -> None:
+    def __init__(self, config, int8: bool = False) -> None:
         super().__init__()
         self.config = config
         self.layers = nn.ModuleList(
-            [TransformerBlock(config.d_model, config.num_heads, config.ffn_dim)
+            [TransformerBlock(config.d_model, config.num_heads, config.ffn_dim, int8=int8)
              for _ in range(config.num_layers)])
         self.final_norm = nn.LayerNorm(config.d_model)
 
