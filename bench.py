@@ -182,8 +182,6 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
     w = W.CONFIGS[name]
     dev = torch.device("cuda:0")
     params = W.make_params(w)
-    if (half or full) and w.int8:
-        raise ValueError("--attention-half / --full-block cover the 16-bit / fp32 configurations")
     ffn_dim = 4 * w.d_model
     if w.int8:
         mod = Int8SelfAttention(w.d_model, w.heads)
@@ -199,10 +197,18 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
     valid = torch.ones(w.batch, w.seq, dtype=torch.bool, device=dev)
     if full:
         torch.manual_seed(W.WEIGHT_SEED + 1)  # norm / FFN parameters: nn.LayerNorm / nn.Linear init
-        blk = TransformerBlock(w.d_model, w.heads, ffn_dim)
+        blk = TransformerBlock(w.d_model, w.heads, ffn_dim, int8=w.int8)
         blk.attention.load_state_dict(params)
-        blk = blk.to(device=dev, dtype=w.dtype).eval()
-        stages = ["norm", "qkv", "attn", "out", "norm2", "ffn_in", "ffn_out"]
+        if w.int8:
+            # W8A8: int8 weights from the fp32 masters; the norms in the activation dtype
+            blk = blk.to(dev).eval()
+            blk.norm1.to(w.dtype)
+            blk.norm2.to(w.dtype)
+            stages = ["norm", "quant_x", "qkv", "attn", "quant_ctx", "out", "norm2", "quant_h2",
+                      "ffn_in", "quant_g", "ffn_out"]
+        else:
+            blk = blk.to(device=dev, dtype=w.dtype).eval()
+            stages = ["norm", "qkv", "attn", "out", "norm2", "ffn_in", "ffn_out"]
 
         def step(marks=None):
             return block_forward(blk, x, valid, w.causal, marks=marks)
@@ -253,9 +259,14 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
             unfused_ms = u0.elapsed_time(u1) / steps
         if full:
             # the FFN half as torch ops (the reference's code) after the fused attention half
+            # (int8: the W8A8 attention half, then the FFN in the activation dtype)
+            f_in = [t.detach().to(w.dtype) for t in (blk.ffn_in.weight, blk.ffn_in.bias)]
+            f_out = [t.detach().to(w.dtype) for t in (blk.ffn_out.weight, blk.ffn_out.bias)]
+
             def torch_ffn_block():
                 x1 = blk.attention.forward_residual(x, blk.norm1, valid, w.causal)
-                y = x1 + blk.ffn_out(F.gelu(blk.ffn_in(blk.norm2(x1)), approximate="none"))
+                hid = F.gelu(F.linear(blk.norm2(x1), *f_in), approximate="none")
+                y = x1 + F.linear(hid, *f_out)
                 return y.masked_fill(~valid[..., None], 0)
             for _ in range(max(3, warmup // 4)):
                 torch_ffn_block()
@@ -302,8 +313,13 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         fl["ffn_in"] = 2.0 * T * d * ffn_dim
         fl["ffn_out"] = 2.0 * T * ffn_dim * d
         by["norm2"] = 2 * act
-        by["ffn_in"] = (T * d + ffn_dim * d) * e + 4 * ffn_dim + T * ffn_dim * e
-        by["ffn_out"] = (T * ffn_dim + d * ffn_dim) * e + 4 * d + 2 * T * d * e
+        if w.int8:
+            # int8 operands and their fp32 scales in, activation-dtype outputs (+ residual read)
+            by["ffn_in"] = T * d + ffn_dim * d + 4 * (T + ffn_dim) + 4 * ffn_dim + T * ffn_dim * e
+            by["ffn_out"] = T * ffn_dim + d * ffn_dim + 4 * (T + d) + 4 * d + 2 * T * d * e
+        else:
+            by["ffn_in"] = (T * d + ffn_dim * d) * e + 4 * ffn_dim + T * ffn_dim * e
+            by["ffn_out"] = (T * ffn_dim + d * ffn_dim) * e + 4 * d + 2 * T * d * e
     stage_ms = {}
     for i, s in enumerate(stages):
         nxt = marks_order[i + 1]
