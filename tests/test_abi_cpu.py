@@ -136,6 +136,19 @@ def test_int8_argument_validation():
     assert h.mi355_gemm_i8(fake, fake, fake, fake, None, 1, fake, 64, None, 4, 64, 40, None, None) == codes["MI355_E_ALIGNMENT"]
     assert h.mi355_gemm_i8(fake, fake, None, fake, None, 1, fake, 64, None, 4, 64, 64, None, None) == codes["MI355_E_NULL_POINTER"]
     assert h.mi355_gemm_i8(fake, fake, fake, fake, None, 9, fake, 64, None, 4, 64, 64, None, None) == codes["MI355_E_BAD_DTYPE"]
+    # the epilogue variant: A, W, s_a, s_w, bias, out_dtype, C, ldc, R, ldr, M, N, K, row_valid,
+    # epi, stream (every rejected call returns before any launch)
+    ep = h.mi355_gemm_i8_epilogue
+    gelu, zero = L.EPI_GELU, L.EPI_ZERO_MASKED
+    assert ep(fake, fake, fake, fake, None, 1, fake, 64, None, 64, 4, 64, 40, None, gelu, None) == codes["MI355_E_ALIGNMENT"]
+    assert ep(fake, fake, fake, fake, None, 1, fake, 64, fake, 64, 4, 64, 64, None, gelu, None) == codes["MI355_E_UNSUPPORTED"]
+    assert ep(fake, fake, fake, fake, None, 1, fake, 64, None, 64, 4, 64, 64, None, 4, None) == codes["MI355_E_UNSUPPORTED"]
+    assert ep(fake, fake, fake, None, None, 1, fake, 64, fake, 64, 4, 64, 64, None, zero, None) == codes["MI355_E_NULL_POINTER"]
+    assert ep(fake, fake, fake, fake, None, 1, None, 64, fake, 64, 4, 64, 64, None, 0, None) == codes["MI355_E_NULL_POINTER"]
+    assert ep(fake, fake, fake, fake, None, 9, fake, 64, fake, 64, 4, 64, 64, None, 0, None) == codes["MI355_E_BAD_DTYPE"]
+    assert ep(fake, fake, fake, fake, None, 1, fake, 64, fake, 32, 4, 64, 64, None, zero, None) == codes["MI355_E_BAD_SIZE"]
+    assert ep(fake, fake, fake, fake, None, 1, fake, 32, None, 64, 4, 64, 64, None, gelu, None) == codes["MI355_E_BAD_SIZE"]
+    assert ep(fake, fake, fake, fake, None, 1, fake, 64, None, 64, 0, 64, 64, None, gelu, None) == 0
 
 
 def test_kernel_error_carries_status():
