@@ -59,6 +59,13 @@ def parse_args():
                     help="time replays of one step captured in a HIP graph (torch.cuda.CUDAGraph): "
                          "no per-kernel host launch cost; the per-stage breakdown still comes from "
                          "the eager loop")
+    ap.add_argument("--official", default="",
+                    help="instead of the attention-block configurations, time the whole model "
+                         "(Transformer on the kernels, eager and graph-replayed) at the benchmark's "
+                         "official shapes (Project/shapes.json): comma-separated ids or 'all', "
+                         "beside the reference's model as torch ops")
+    ap.add_argument("--dtype", default="float32", choices=("float32", "float16", "bfloat16"),
+                    help="model dtype of --official (the benchmark's default is float32)")
     ap.add_argument("--copy-calibration", type=int, default=0, metavar="BYTES",
                     help="only run a plain copy kernel (y = -x, fp16) over BYTES bytes, three times; "
                          "profiled with rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE it calibrates the "
@@ -380,6 +387,102 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
     return result
 
 
+def torch_model_forward(model, x, mask, causal):
+    """The reference's model as torch ops (BaselineTransformer.forward and its blocks,
+    torch_transformer_benchmark.py:85-172) on ``model``'s parameters: the comparison path of
+    --official. Transposed operands of the batched products are made contiguous first."""
+    import torch
+    import torch.nn.functional as F
+    B, S, d = x.shape
+    causal_mask = torch.ones(S, S, dtype=torch.bool, device=x.device).triu(1) if causal else None
+    for blk in model.layers:
+        a = blk.attention
+        h = F.layer_norm(x, (d,), blk.norm1.weight, blk.norm1.bias, blk.norm1.eps)
+        q, k, v = (F.linear(h, lin.weight, lin.bias).view(B, S, a.num_heads, a.head_dim)
+                   .transpose(1, 2).contiguous() for lin in (a.q_proj, a.k_proj, a.v_proj))
+        s = torch.matmul(q, k.transpose(-2, -1).contiguous()) * a.scale
+        if causal_mask is not None:
+            s = s.masked_fill(causal_mask, float("-inf"))
+        if mask is not None:
+            s = s.masked_fill(~mask[:, None, None, :], float("-inf"))
+        p = torch.softmax(s.float(), dim=-1).to(x.dtype)
+        ctx = torch.matmul(p, v).transpose(1, 2).reshape(B, S, d)
+        o = F.linear(ctx, a.out_proj.weight, a.out_proj.bias)
+        if mask is not None:
+            o = o.masked_fill(~mask[..., None], 0)
+        x = x + o
+        f = F.linear(F.gelu(F.linear(F.layer_norm(x, (d,), blk.norm2.weight, blk.norm2.bias,
+                                                  blk.norm2.eps), blk.ffn_in.weight,
+                                     blk.ffn_in.bias), approximate="none"),
+                     blk.ffn_out.weight, blk.ffn_out.bias)
+        x = x + f
+        if mask is not None:
+            x = x.masked_fill(~mask[..., None], 0)
+    fn = model.final_norm
+    x = F.layer_norm(x, (d,), fn.weight, fn.bias, fn.eps)
+    return x if mask is None else x.masked_fill(~mask[..., None], 0)
+
+
+def measure_official(sid: int, dtype_name: str, steps: int, warmup: int) -> dict:
+    """One model forward at official shape ``sid`` with the harness's all-true mask
+    (generate_random_case, torch_transformer_benchmark.py:234-272), on the kernels (eager and
+    replayed from a graph) and as the reference's torch ops."""
+    import torch
+    from types import SimpleNamespace
+    from tiktok_techjam_2026_track3_amd import Transformer
+    from tiktok_techjam_2026_track3_amd import workloads as W
+    B, d, H, S, L, F_ = W.OFFICIAL_SHAPES[sid]
+    dtype = getattr(torch, dtype_name)
+    cfg = SimpleNamespace(batch_size=B, seq_len=S, d_model=d, num_heads=H, ffn_dim=F_,
+                          num_layers=L, causal=True)
+    torch.manual_seed(1234)
+    model = Transformer(cfg).to(device="cuda", dtype=dtype).eval()
+    g = torch.Generator(device="cuda").manual_seed(1234 + 100000)
+    x = torch.randn(B, S, d, device="cuda", generator=g).to(dtype)
+    mask = torch.ones(B, S, dtype=torch.bool, device="cuda")
+
+    def timed(fn):
+        with torch.inference_mode():
+            for _ in range(warmup):
+                fn()
+            torch.cuda.synchronize()
+            e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            e0.record()
+            for _ in range(steps):
+                fn()
+            e1.record()
+            torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / steps
+
+    ours = timed(lambda: model(x, mask))
+    with torch.inference_mode():
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            model(x, mask)
+        torch.cuda.current_stream().wait_stream(side)
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            model(x, mask)
+    replay = timed(graph.replay)
+    ref = None
+    if sid != 14:  # the dense S x S scores of shape 14 (multi-TB) do not fit: Project/shapes.json
+        ref = timed(lambda: torch_model_forward(model, x, mask, True))
+    fl = W.official_flops(sid)
+    best = min(ours, replay)
+    return {
+        "metric": "official-shape model forward ms/iter (Transformer on the kernels)",
+        "value": round(best, 5), "unit": "ms", "higher_is_better": False, "n_gpus": 1,
+        "steps": steps, "warmup": warmup, "dtype": dtype_name, "data": "synthetic",
+        "config": {"workload": f"official shape {sid}", "batch": B, "d_model": d, "heads": H,
+                   "seq_len": S, "layers": L, "ffn_dim": F_, "causal": True},
+        "eager_ms": round(ours, 5), "graph_replay_ms": round(replay, 5),
+        "torch_ops_ms": None if ref is None else round(ref, 5),
+        "speedup_vs_torch_ops": None if ref is None else round(ref / best, 3),
+        "tflops": round(fl / best / 1e9, 2),
+    }
+
+
 def main() -> int:
     args = parse_args()
     if args.gpus != 1:
@@ -395,6 +498,21 @@ def main() -> int:
         print(json.dumps(copy_calibration(args.copy_calibration)), flush=True)
         return 0
     from tiktok_techjam_2026_track3_amd import workloads as W
+
+    if args.official:
+        ids = (sorted(W.OFFICIAL_SHAPES) if args.official == "all"
+               else [int(t) for t in args.official.split(",") if t.strip()])
+        for sid in ids:
+            if sid not in W.OFFICIAL_SHAPES:
+                log(f"unknown official shape {sid}")
+                return 2
+            if sid == 14 and args.dtype == "float32":
+                log("[bench] official shape 14 runs in 16-bit only (fp32 attention at S=100000 "
+                    "is the vector-ALU kernel, minutes per forward); use --dtype float16")
+                continue
+            log(f"[bench] official shape {sid} ({args.dtype})")
+            print(json.dumps(measure_official(sid, args.dtype, args.steps, args.warmup)), flush=True)
+        return 0
 
     rc = 0
     for name in [c.strip() for c in args.config.split(",") if c.strip()]:

@@ -129,3 +129,23 @@ def make_input(w: Workload, seed: int, device: str = "cpu", input_scale: float =
 def round_params(params: Dict[str, torch.Tensor], dtype: torch.dtype) -> Dict[str, torch.Tensor]:
     """Parameters rounded to ``dtype`` (what a ``model.to(dtype)`` holds)."""
     return {k: v.to(dtype) for k, v in params.items()}
+
+
+# The benchmark's 14 official shapes (Project/shapes.json, "3.7 Appendix Test shapes" of the
+# reference README): id -> (batch, d_model, heads, seq_len, layers, ffn_dim); every one causal,
+# run by torch_transformer_benchmark.py in float32 unless --dtype says otherwise.
+OFFICIAL_SHAPES = {
+    1: (64, 128, 4, 128, 4, 128), 2: (1, 128, 4, 128, 4, 128), 3: (4, 128, 4, 128, 4, 128),
+    4: (16, 128, 4, 128, 4, 128), 5: (128, 128, 4, 128, 4, 128), 6: (10000, 128, 4, 128, 4, 128),
+    7: (64, 32, 4, 128, 4, 32), 8: (64, 1024, 4, 128, 4, 1024), 9: (64, 128, 1, 128, 4, 128),
+    10: (64, 128, 2, 128, 4, 128), 11: (64, 128, 16, 128, 4, 128), 12: (64, 128, 4, 32, 4, 128),
+    13: (64, 128, 4, 1024, 4, 128), 14: (32, 1024, 16, 100000, 2, 1024),
+}
+
+
+def official_flops(sid: int) -> float:
+    """Algorithmic FLOPs of one model forward at an official shape: per layer the four
+    projections (8 T d^2), the FFN (4 T d f) and causal attention (2 B S^2 d)."""
+    B, d, H, S, L, F = OFFICIAL_SHAPES[sid]
+    T = B * S
+    return L * (8.0 * T * d * d + 4.0 * T * d * F + 2.0 * B * S * S * d)
