@@ -25,6 +25,7 @@ from oracle import block as OB
 from oracle import int8 as OI
 from oracle import model as OM
 from oracle.predicate import compare_outputs
+from tiktok_techjam_2026_track3_amd import workloads as W
 
 pytestmark = pytest.mark.gpu
 
@@ -236,17 +237,11 @@ def test_transformer_matches_oracle_block_by_block(gpu, dtype, causal, masked):
     _check_block_by_block(gpu, cfg, dtype, [320, 201] if masked else None)
 
 
-# The benchmark's 14 official shapes (Project/shapes.json: id, batch, d_model, heads, seq_len,
-# layers, ffn_dim; every one causal), run by torch_transformer_benchmark.py in float32 unless
-# --dtype says otherwise. Head dims: 32 (d128/4 heads), 8 (d32/4, d128/16), 256 (d1024/4),
-# 128 (d128/1), 64 (d128/2, d1024/16).
-OFFICIAL_SHAPES = [
-    (1, 64, 128, 4, 128, 4, 128), (2, 1, 128, 4, 128, 4, 128), (3, 4, 128, 4, 128, 4, 128),
-    (4, 16, 128, 4, 128, 4, 128), (5, 128, 128, 4, 128, 4, 128), (6, 10000, 128, 4, 128, 4, 128),
-    (7, 64, 32, 4, 128, 4, 32), (8, 64, 1024, 4, 128, 4, 1024), (9, 64, 128, 1, 128, 4, 128),
-    (10, 64, 128, 2, 128, 4, 128), (11, 64, 128, 16, 128, 4, 128), (12, 64, 128, 4, 32, 4, 128),
-    (13, 64, 128, 4, 1024, 4, 128), (14, 32, 1024, 16, 100000, 2, 1024),
-]
+# The benchmark's 14 official shapes (Project/shapes.json; every one causal), run by
+# torch_transformer_benchmark.py in float32 unless --dtype says otherwise. Head dims: 32 (d128/4
+# heads), 8 (d32/4, d128/16), 256 (d1024/4), 128 (d128/1), 64 (d128/2, d1024/16).
+OFFICIAL_SHAPES = [(sid, *dims) for sid, dims in sorted(W.OFFICIAL_SHAPES.items())]
+# (id, batch, d_model, heads, seq_len, layers, ffn_dim)
 
 
 def _official_cfg(shape, max_batch, max_seq):
