@@ -205,6 +205,21 @@ def test_attention_other_head_dims(gpu, dtype, hd, causal, S):
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 @pytest.mark.parametrize("hd", [8, 32, 256])
 @pytest.mark.parametrize("causal", [False, True])
+def test_attention_short_keys_many_tiles(gpu, dtype, hd, causal):
+    """Up to 256 keys and at least 1024 query tiles: the vector-ALU kernel splits each tile's
+    keys over 2 waves instead of 8 (B 48, H 8, S 100: 1536 to 4992 tiles), with and without a
+    key mask."""
+    B, S = 48, 100
+    g = torch.Generator().manual_seed(hd + 7)
+    mask = torch.rand(B, S, generator=g) > 0.2
+    mask[:, 0] = True
+    _attn_check(gpu, dtype, B, 8, S, S, hd, causal, seed=51)
+    _attn_check(gpu, dtype, B, 8, S, S, hd, causal, key_valid=mask, seed=52)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("hd", [8, 32, 256])
+@pytest.mark.parametrize("causal", [False, True])
 def test_attention_other_head_dims_masked_packed(gpu, dtype, hd, causal):
     B, S = 3, 130
     g = torch.Generator().manual_seed(hd)

@@ -840,9 +840,8 @@ int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
   return static_cast<int>(hipGetLastError());
 }
 
-template <typename T, int HD>
-int launch_valu(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
-  constexpr int NWK = 8;  // waves (key ranges) per query tile
+template <typename T, int HD, int NWK>
+int launch_valu_nwk(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
   constexpr int QT = ValuShape<HD>::QT;
   AttnArgs a = a0;
   a.n_qtiles = static_cast<int>((a.Sq + QT - 1) / QT);
@@ -861,6 +860,18 @@ int launch_valu(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
     else hipLaunchKernelGGL((attn_fwd_valu<T, HD, false, false, NWK>), grid, block, 0, s, a);
   }
   return static_cast<int>(hipGetLastError());
+}
+
+// NWK waves split a query tile's keys: 2 up to 256 keys when there are at least 1024 query tiles
+// (two waves for every SIMD), where eight ranges would leave each wave one or two chunks and the
+// partial-state merge would dominate (official shape 6: -17% per forward); 8 otherwise, so long
+// key ranges and small grids (one sequence of 128 tokens: 32 tiles) keep every CU busy
+template <typename T, int HD>
+int launch_valu(const AttnArgs& a, bool causal, bool kmask, hipStream_t s) {
+  constexpr int QT = ValuShape<HD>::QT;
+  const int64_t tiles = (a.Sq + QT - 1) / QT * a.H * a.B;
+  if (a.Sk <= 256 && tiles >= 1024) return launch_valu_nwk<T, HD, 2>(a, causal, kmask, s);
+  return launch_valu_nwk<T, HD, 8>(a, causal, kmask, s);
 }
 
 // head dims of the VALU kernel (fp32: all of them; 16-bit: all but 64 and 128, which the MFMA
