@@ -4,17 +4,23 @@ on one MI355X.
 
 A step is one forward of the block over one batch of synthetic input already resident in HBM,
 with the all-true validity mask the reference's timing loop passes
-(torch_transformer_benchmark.py:529-536). The default workload is configuration C2
-(B8 S2048 d1024 H16x64 fp16, non-causal); ``--config`` selects another (C1..C5, comma list).
+(torch_transformer_benchmark.py:529-536). ``--config`` takes a comma list of C1..C5, each
+optionally suffixed with a mode: ``:core`` times the attention core alone on its own inputs
+(C5 as BASELINE states it: Q, K, V ~ N(0, 1) / sqrt(head_dim)), ``:half`` the attention half
+x + attention(norm1(x)), ``:full`` the whole transformer block. The default runs C1..C4 (block),
+C5 (block) and, as its last line, C5:core -- the configuration the >=60% MFMA target is stated
+on.
 
-Untimed warm-up: ``--warmup`` steps, continued until at least ``--min-warmup-s`` seconds of
-back-to-back steps have run (the GPU's clocks ramp over a few hundred milliseconds), then exactly
-``--steps`` timed steps.
+Timing follows the reference's protocol (torch_transformer_benchmark.py:463-583): untimed
+warm-up (``--warmup`` steps, continued until ``--min-warmup-s`` seconds of back-to-back steps
+have run so clocks have ramped), then the ``--steps`` timed steps split into 3 rounds, every
+step bracketed by its own HIP events on the launch stream and every round by device
+synchronisation; ``ms_per_step`` is the median step. Per-kernel averages come from events
+recorded around every launch inside the same steps; the dominant kernel's roofline uses them.
 
-Printed (stdout, one JSON line per configuration): whole-block TFLOP/s and ms/step over the timed
-steps (HIP events on the launch stream, bracketed by device synchronisation), per-kernel averages
-from events recorded around every launch inside the timed region, the roofline of the dominant
-kernel, and the CPU oracle timed on a bounded sample on this host.
+Printed (stdout, one JSON line per configuration): whole-step TFLOP/s (TOP/s for int8) at the
+median, the per-kernel breakdown, the roofline of the dominant kernel, and the CPU oracle timed
+on a bounded sample on this host's cores.
 """
 from __future__ import annotations
 
@@ -36,15 +42,22 @@ def log(*a):
 def parse_args():
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=100)
-    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--steps", type=int, default=None,
+                    help="timed steps per configuration (default: 60, or 9 for C5)")
+    ap.add_argument("--warmup", type=int, default=None,
+                    help="untimed warm-up steps (default: 20, or 2 for C5)")
     ap.add_argument("--min-warmup-s", type=float, default=0.5,
                     help="keep warming up (untimed) until this many seconds of back-to-back steps "
                          "have run, so the timed steps see sustained clocks")
-    ap.add_argument("--config", default="C2", help="C1..C5 or a comma-separated list")
-    ap.add_argument("--cpu-budget", type=float, default=20.0,
+    ap.add_argument("--config", default="C1,C2,C3,C4,C5,C5:core",
+                    help="comma list of C1..C5, each optionally suffixed :core, :half or :full")
+    ap.add_argument("--rounds", type=int, default=3,
+                    help="the timed steps are split into this many rounds (reference: 3)")
+    ap.add_argument("--cpu-budget", type=float, default=15.0,
                     help="approximate seconds of CPU-oracle work for the cpu_baseline leg")
     ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--core", action="store_true",
+                    help="time the attention core alone (mode :core for every listed config)")
     ap.add_argument("--attention-half", action="store_true",
                     help="time the block's whole attention half instead, x + attention(norm1(x)) "
                          "(torch_transformer_benchmark.py:139): LayerNorm kernel, QKV projection, "
@@ -110,79 +123,124 @@ def cpu_model() -> str:
     return "unknown"
 
 
+def host_cores() -> dict:
+    """Core counts of this host as the process sees them: os.cpu_count(), the CPUs the process
+    may run on (affinity), the cgroup CPU quota (cpu.max) if one is set, and the lscpu model."""
+    info = {"os_cpu_count": os.cpu_count()}
+    try:
+        info["affinity"] = len(os.sched_getaffinity(0))
+    except (AttributeError, OSError):
+        info["affinity"] = os.cpu_count()
+    quota = None
+    try:
+        q, period = open("/sys/fs/cgroup/cpu.max").read().split()[:2]
+        if q != "max":
+            quota = max(1, int(int(q) / int(period)))
+    except (OSError, ValueError):
+        pass
+    info["cgroup_quota_cpus"] = quota
+    model = None
+    try:
+        import subprocess
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            if line.startswith("Model name:"):
+                model = line.split(":", 1)[1].strip()
+    except Exception:  # noqa: BLE001 -- lscpu is informational only
+        pass
+    info["lscpu_model"] = model or cpu_model()
+    return info
+
+
 # ------------------------------------------------------------------------------- cpu baseline
-def cpu_baseline(w, budget_s: float) -> dict:
-    """Times the CPU oracle (the reference path restated in torch-CPU fp32) on one batch row:
-    the QKV projection of all its tokens (the keys and values every query needs), attention for
-    ``n_q`` query rows spread over the sequence, and the output projection of those rows.
-    Reports its operation rate in the metric's unit."""
+def cpu_baseline(w, budget_s: float, core: bool = False) -> dict:
+    """Times the CPU oracle (the reference path restated in torch-CPU fp32) on a bounded sample
+    of one batch row: the QKV projection of all its tokens (the keys and values every query
+    needs), attention for ``n_q`` query rows spread over the sequence (the whole row when it is
+    short), and the output projection of those rows; ``core`` times the attention of those rows
+    alone on the core's own inputs. Every core this process may use (capped by the cgroup CPU
+    quota) runs torch's CPU kernels. Reports the operation rate in the metric's unit."""
     import torch
     from oracle import attention as OA
     from oracle import int8 as OI
     from oracle import streamed as OS
     from tiktok_techjam_2026_track3_amd import workloads as W
 
-    threads = min(os.cpu_count() or 1, 16)
+    hc = host_cores()
+    threads = hc["affinity"] or 1
+    if hc["cgroup_quota_cpus"]:
+        threads = min(threads, hc["cgroup_quota_cpus"])
     torch.set_num_threads(threads)
     S, d, H, hd = w.seq, w.d_model, w.heads, w.head_dim
     row = w.scaled(batch=1)
-    params = W.make_params(w)
-    if not w.int8:
-        params = W.round_params(params, w.dtype)
-    pf = {k: v.float() for k, v in params.items()}
-    x = W.make_input(row, W.TIMING_SEED).float()
-
-    # query rows per sample: whole row when the dense oracle fits, otherwise a spread subset
     n_q = S if S <= 4096 else 256
     idx = torch.linspace(0, S - 1, n_q).round().long() if n_q < S else torch.arange(S)
-
-    def one():
-        if w.int8:
-            return OI.int8_self_attention(x.to(torch.float16), params, H, w.causal)["out"]
-        if n_q == S:
-            return OA.self_attention(x, pf, H, causal=w.causal)
-        qkv = OA.qkv_projection(x, pf).view(1, S, 3, H, hd)
-        q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
-        ctx = OS.streamed_attention_core(q[:, :, idx], k, v, hd ** -0.5, w.causal, q_index=idx)
-        ctx = ctx.transpose(1, 2).reshape(1, n_q, d)
-        return torch.nn.functional.linear(ctx, pf["out_proj.weight"], pf["out_proj.bias"])
-
     attn_pairs = float(((idx + 1).sum() if w.causal else n_q * S))
-    flops = 2.0 * S * d * 3 * d + 4.0 * H * hd * attn_pairs + 2.0 * n_q * d * d
+    if core:
+        q, k, v = (t.float().permute(0, 2, 1, 3).contiguous()
+                   for t in W.make_core_inputs(row, W.TIMING_SEED))
+
+        def one():
+            return OS.streamed_attention_core(q[:, :, idx], k, v, hd ** -0.5, w.causal, q_index=idx)
+        flops = 4.0 * H * hd * attn_pairs
+        what = (f"{w.name} core, batch row 0 of {w.batch}: {'causal ' if w.causal else ''}"
+                f"streamed attention of {n_q} query rows x {H} heads over all {S} keys; ")
+    else:
+        params = W.make_params(w)
+        if not w.int8:
+            params = W.round_params(params, w.dtype)
+        pf = {kk: vv.float() for kk, vv in params.items()}
+        x = W.make_input(row, W.TIMING_SEED).float()
+
+        def one():
+            if w.int8:
+                return OI.int8_self_attention(x.to(torch.float16), params, H, w.causal)["out"]
+            if n_q == S:
+                return OA.self_attention(x, pf, H, causal=w.causal)
+            qkv = OA.qkv_projection(x, pf).view(1, S, 3, H, hd)
+            q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
+            ctx = OS.streamed_attention_core(q[:, :, idx], k, v, hd ** -0.5, w.causal, q_index=idx)
+            ctx = ctx.transpose(1, 2).reshape(1, n_q, d)
+            return torch.nn.functional.linear(ctx, pf["out_proj.weight"], pf["out_proj.bias"])
+        flops = 2.0 * S * d * 3 * d + 4.0 * H * hd * attn_pairs + 2.0 * n_q * d * d
+        what = (f"{w.name} batch row 0 of {w.batch}: QKV projection of all {S} tokens, "
+                f"{'causal ' if w.causal else ''}attention of {n_q} query rows x {H} heads, out "
+                f"projection of those rows; {'int8 recipe (numpy) + ' if w.int8 else ''}")
     times = []
     t_all = time.perf_counter()
     with torch.inference_mode():
         while True:
-            t0 = time.perf_counter()
+            t0 = time.perf_counter_ns()
             one()
-            times.append(time.perf_counter() - t0)
-            if time.perf_counter() - t_all > budget_s or len(times) >= 4:
+            times.append((time.perf_counter_ns() - t0) / 1e9)
+            # about budget_s seconds of CPU work, at least 3 calls (bounded for tiny samples)
+            if (time.perf_counter() - t_all > budget_s and len(times) >= 3) or len(times) >= 500:
                 break
     # the first call carries one-time costs when more than one call fit in the budget
     timed = times[1:] if len(times) > 1 else times
     timed.sort()
     med = timed[len(timed) // 2]
-    unit = "TOP/s" if w.int8 else "TFLOP/s"
+    unit = "TOP/s" if (w.int8 and not core) else "TFLOP/s"
     return {
         "value": flops / med / 1e12,
         "unit": unit,
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"{w.name} batch row 0 of {w.batch}: QKV projection of all {S} tokens, "
-                   f"{'causal ' if w.causal else ''}attention of {n_q} query rows x {H} heads, out "
-                   f"projection of those rows; {'int8 recipe (numpy) + ' if w.int8 else ''}"
-                   f"torch-CPU fp32 oracle; median of {len(timed)} of {len(times)} calls, "
-                   f"{med * 1e3:.1f} ms/call, {flops / 1e9:.1f} G{'OP' if w.int8 else 'FLOP'}/call"),
-        "cpu": cpu_model(),
+        "sample": (f"{what}torch-CPU fp32 oracle; median of {len(timed)} of {len(times)} calls "
+                   f"(time.perf_counter_ns per call), {med * 1e3:.1f} ms/call, "
+                   f"{flops / 1e9:.1f} G{'OP' if unit == 'TOP/s' else 'FLOP'}/call"),
+        "host": hc,
     }
 
 
 # ------------------------------------------------------------------------------ gpu measure
 def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
-            half: bool = False, graph: bool = False, full: bool = False) -> dict:
+            half: bool = False, graph: bool = False, full: bool = False, core: bool = False,
+            rounds: int = 3) -> dict:
     import torch
     import torch.nn.functional as F
     from tiktok_techjam_2026_track3_amd import Int8SelfAttention, SelfAttention, TransformerBlock
+    from tiktok_techjam_2026_track3_amd import ops
     from tiktok_techjam_2026_track3_amd import workloads as W
     from tiktok_techjam_2026_track3_amd.transformer import block_forward
 
@@ -190,7 +248,9 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
     dev = torch.device("cuda:0")
     params = W.make_params(w)
     ffn_dim = 4 * w.d_model
-    if w.int8:
+    if core:
+        stages = ["attn"]
+    elif w.int8:
         mod = Int8SelfAttention(w.d_model, w.heads)
         mod.load_state_dict(params)
         mod = mod.to(dev)
@@ -200,9 +260,22 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         mod.load_state_dict(params)
         mod = mod.to(device=dev, dtype=w.dtype)
         stages = ["qkv", "attn", "out"]
-    x = W.make_input(w, W.TIMING_SEED, device="cuda")
+    if core:
+        qc, kc, vc = W.make_core_inputs(w, W.TIMING_SEED, device="cuda")
+        oc = torch.empty_like(qc)
+        x = qc
+    else:
+        x = W.make_input(w, W.TIMING_SEED, device="cuda")
     valid = torch.ones(w.batch, w.seq, dtype=torch.bool, device=dev)
-    if full:
+    if core:
+        def step(marks=None):
+            if marks:
+                marks("attn")
+            ops.attention(qc, kc, vc, out=oc, causal=w.causal)
+            if marks:
+                marks("end")
+            return oc
+    elif full:
         torch.manual_seed(W.WEIGHT_SEED + 1)  # norm / FFN parameters: nn.LayerNorm / nn.Linear init
         blk = TransformerBlock(w.d_model, w.heads, ffn_dim, int8=w.int8)
         blk.attention.load_state_dict(params)
@@ -230,25 +303,32 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
             return mod.run(x, valid, w.causal, marks=marks)
 
     marks_order = stages + ["end"]
-    events = [{s: torch.cuda.Event(enable_timing=True) for s in marks_order} for _ in range(steps)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    events = [{s: torch.cuda.Event(enable_timing=True) for s in ["start"] + marks_order}
+              for _ in range(steps)]
+    # the timed steps in `rounds` rounds, each bracketed by device synchronisation; every step
+    # has its own start / end events on the launch stream (benchmark_once, :477-508)
+    n_rounds = max(1, min(rounds, steps))
+    per_round = [steps // n_rounds + (1 if r < steps % n_rounds else 0) for r in range(n_rounds)]
     with torch.inference_mode():
         t_w = time.perf_counter()
         n_warm = 0
         while n_warm < warmup or time.perf_counter() - t_w < min_warmup_s:
             step()
             n_warm += 1
-            if n_warm % 8 == 0:
+            if n_warm % 8 == 0 or core:
                 torch.cuda.synchronize()  # tie the wall clock to the GPU's progress
         torch.cuda.synchronize()
         warm_s = time.perf_counter() - t_w
         t0 = time.perf_counter()
-        start.record()
-        for k in range(steps):
-            ev = events[k]
-            step(marks=lambda s, ev=ev: ev[s].record())
-        end.record()
-        torch.cuda.synchronize()
+        k = 0
+        for n_r in per_round:
+            torch.cuda.synchronize()
+            for _ in range(n_r):
+                ev = events[k]
+                ev["start"].record()
+                step(marks=lambda s, ev=ev: ev[s].record())
+                k += 1
+            torch.cuda.synchronize()
         wall = time.perf_counter() - t0
         unfused_ms = None
         if half:
@@ -285,7 +365,13 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
             u1.record()
             torch.cuda.synchronize()
             unfused_ms = u0.elapsed_time(u1) / steps
-    ms_step = start.elapsed_time(end) / steps
+    samples = sorted(events[k]["start"].elapsed_time(events[k]["end"]) for k in range(steps))
+    ms_step = samples[len(samples) // 2] if steps % 2 else 0.5 * (samples[steps // 2 - 1] + samples[steps // 2])
+    timing = {"median_ms": round(ms_step, 5), "mean_ms": round(sum(samples) / steps, 5),
+              "p90_ms": round(samples[min(steps - 1, int(0.9 * steps))], 5),
+              "min_ms": round(samples[0], 5), "rounds": per_round,
+              "protocol": "per-step HIP events on the launch stream, rounds bracketed by device "
+                          "synchronisation, median (torch_transformer_benchmark.py:463-583)"}
     eager_ms = ms_step
     if graph:
         # one step captured once (after a side-stream warm-up, as capture requires), then replayed
@@ -310,6 +396,10 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         ms_step = g0.elapsed_time(g1) / steps
     fl = dict(w.flops())
     by = dict(w.bytes())
+    if core:
+        cf, cb = W.core_flops_bytes(w)
+        fl = {"attn": cf}
+        by = {"attn": cb}
     if half or full:
         act = w.tokens * w.d_model * x.element_size()
         by["norm"] = 2 * act                      # read x, write norm1(x)
@@ -331,7 +421,8 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
     for i, s in enumerate(stages):
         nxt = marks_order[i + 1]
         stage_ms[s] = sum(events[k][s].elapsed_time(events[k][nxt]) for k in range(steps)) / steps
-    total_ops = fl["qkv"] + fl["attn"] + fl["out"] + fl.get("ffn_in", 0.0) + fl.get("ffn_out", 0.0)
+    total_ops = (fl.get("qkv", 0.0) + fl["attn"] + fl.get("out", 0.0) + fl.get("ffn_in", 0.0)
+                 + fl.get("ffn_out", 0.0))
     dt = DTYPE_NAME[str(w.dtype)]
     stage_report = {}
     for s, ms in stage_ms.items():
@@ -349,12 +440,13 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         kdt = "fp16" if (w.int8 or w.dtype == torch.bfloat16) else dt
         peak = PEAKS_TFLOPS[kdt]
     achieved = fl[dom] / stage_ms[dom] / 1e9
+    mode = "core" if core else ("full" if full else ("half" if half else "block"))
     kernel_name = {"qkv": "gemm (QKV projection)", "attn": "attn_fwd", "out": "gemm (out projection)",
                    "ffn_in": "gemm (ffn_in + GELU)", "ffn_out": "gemm (ffn_out + residual)"}[dom]
     result = {
         "metric": "attention-block ms/iter + TFLOP/s (% of MFMA peak) per config, 1 MI355X",
         "value": round(total_ops / ms_step / 1e9, 3),
-        "unit": "TOP/s (int8 GEMMs + fp16 SDPA)" if w.int8 else "TFLOP/s",
+        "unit": "TOP/s (int8 GEMMs + fp16 SDPA)" if (w.int8 and not core) else "TFLOP/s",
         "n_gpus": 1,
         "steps": steps,
         "warmup": warmup,
@@ -362,18 +454,25 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": ("int8+fp16" if w.int8 else ("bf16 projections, fp16 SDPA core" if w.dtype == torch.bfloat16 else dt)),
-        "data": "synthetic (seeded N(0,1) inputs, configuration weight init)",
-        "config": {"workload": f"{w.name}: {w.description}"
+        "dtype": ("fp16" if core and w.int8 else
+                  "int8+fp16" if w.int8 else
+                  ("bf16 projections, fp16 SDPA core" if (w.dtype == torch.bfloat16 and not core) else dt)),
+        "data": ("synthetic (seeded Q, K, V ~ N(0,1)/sqrt(head_dim))" if core else
+                 "synthetic (seeded N(0,1) inputs, configuration weight init)"),
+        "config": {"workload": f"{w.name}{':core' if core else ''}: "
+                               + (f"attention core only (Q, K, V given), {w.description}" if core
+                                  else w.description)
                                + (" + norm1 and residual (attention half of the block)" if half else "")
                                + (f" + norm1/norm2, residuals, FFN {w.d_model}->{ffn_dim}->{w.d_model} "
                                   "with exact GELU (whole transformer block)" if full else ""),
                    "batch": w.batch, "seq_len": w.seq,
                    "d_model": w.d_model, "heads": w.heads, "head_dim": w.head_dim,
-                   "causal": w.causal, "parallelism": "none (1 GPU)"},
+                   "causal": w.causal, "mode": mode, "parallelism": "none (1 GPU)"},
+        "timing": timing,
         "roofline": {"kernel": kernel_name, "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": peak, "unit": "TOP/s" if kdt == "int8" else "TFLOP/s",
-                     "frac": round(achieved / peak, 4), "traffic": measured_traffic(name, dom),
+                     "frac": round(achieved / peak, 4),
+                     "traffic": measured_traffic(name + (":core" if core else ""), dom),
                      "algorithmic_bytes": by[dom], "dtype": kdt},
         "stages": stage_report,
         "wall_s": round(wall, 3),
@@ -515,17 +614,25 @@ def main() -> int:
         return 0
 
     rc = 0
-    for name in [c.strip() for c in args.config.split(",") if c.strip()]:
-        if name not in W.CONFIGS:
-            log(f"unknown config {name}")
+    modes = {"core", "half", "full", "block"}
+    for token in [c.strip() for c in args.config.split(",") if c.strip()]:
+        name, _, mode = token.partition(":")
+        if name not in W.CONFIGS or (mode and mode not in modes):
+            log(f"unknown config {token}")
             return 2
-        log(f"[bench] {name}: warmup {args.warmup}, steps {args.steps}")
-        res = measure(name, args.steps, args.warmup, args.min_warmup_s, args.attention_half,
-                      args.graph, args.full_block)
-        log(f"[bench] {name}: {res['ms_per_step']} ms/step, {res['value']} {res['unit']}")
+        mode = mode or ("core" if args.core else "full" if args.full_block else
+                        "half" if args.attention_half else "block")
+        long_step = name == "C5"
+        steps = args.steps if args.steps is not None else (9 if long_step else 60)
+        warmup = args.warmup if args.warmup is not None else (2 if long_step else 20)
+        log(f"[bench] {token} ({mode}): warmup {warmup}, steps {steps} in {args.rounds} rounds")
+        res = measure(name, steps, warmup, args.min_warmup_s, mode == "half", args.graph,
+                      mode == "full", mode == "core", args.rounds)
+        log(f"[bench] {token}: {res['ms_per_step']} ms/step (median), {res['value']} {res['unit']}, "
+            f"roofline {res['roofline']['kernel']} {res['roofline']['frac']}")
         if not args.no_cpu_baseline:
-            log(f"[bench] {name}: cpu baseline (budget {args.cpu_budget}s)")
-            res["cpu_baseline"] = cpu_baseline(W.CONFIGS[name], args.cpu_budget)
+            log(f"[bench] {token}: cpu baseline (budget {args.cpu_budget}s)")
+            res["cpu_baseline"] = cpu_baseline(W.CONFIGS[name], args.cpu_budget, core=mode == "core")
         else:
             res["cpu_baseline"] = None
         print(json.dumps(res), flush=True)

@@ -22,21 +22,31 @@ import numpy as np
 F32 = np.float32
 
 
+def _to_i8(r: np.ndarray) -> np.ndarray:
+    """``.to(torch.int8)`` of the rounded quotients. They lie in [-127, 127] for finite rows;
+    a NaN (a row holding NaN has a NaN scale, k008:150, torch's amax and clamp propagate it)
+    converts to 0, as the GPU's float-to-integer conversion does."""
+    with np.errstate(invalid="ignore"):
+        return np.where(np.isnan(r), 0, r).astype(np.int8)
+
+
 def quant_rows(t: np.ndarray):
-    """Activation recipe: returns (int8 [N, K], fp32 scale [N])."""
+    """Activation recipe (k008:148-151): returns (int8 [N, K], fp32 scale [N])."""
     t = np.asarray(t, dtype=F32)
-    amax = np.abs(t).max(axis=-1)
-    s = (np.maximum(amax, F32(1e-6)) / F32(127.0)).astype(F32)
-    q = np.rint(t / s[:, None]).astype(np.int8)
-    return q, s
+    amax = np.abs(t).max(axis=-1)                  # NaN-propagating, as torch.amax
+    s = (np.maximum(amax, F32(1e-6)) / F32(127.0)).astype(F32)   # np.maximum keeps NaN, as clamp
+    with np.errstate(invalid="ignore"):
+        r = np.rint(t / s[:, None])
+    return _to_i8(r), s
 
 
 def quant_weight(w: np.ndarray):
-    """Weight recipe: returns (int8 [N, K], fp32 scale [N])."""
+    """Weight recipe (k008:154-158): returns (int8 [N, K], fp32 scale [N])."""
     w = np.asarray(w, dtype=F32)
     s = np.maximum(np.abs(w).max(axis=1) / F32(127.0), F32(1e-8)).astype(F32)
-    q = np.rint(w / s[:, None]).astype(np.int8)
-    return q, s
+    with np.errstate(invalid="ignore"):
+        r = np.rint(w / s[:, None])
+    return _to_i8(r), s
 
 
 def int8_gemm(a_i8: np.ndarray, w_i8: np.ndarray) -> np.ndarray:
@@ -82,7 +92,8 @@ def int8_self_attention(x, params, num_heads: int, causal: bool = False, rows=No
     """The attention half of ``block_forward`` (k008_int8_gemm.py:189-225) on CPU.
 
     x [B, S, d] (fp16 values) -> quantised QKV projection -> fp16 qkv (:197) -> fp32-math
-    attention -> context rounded to fp16 (the fp16 attention output, :207) -> quantised out
+    attention with the probabilities rounded to fp16 before P·V (:108, :218) -> context rounded
+    to fp16 (the fp16 attention output, :207) -> quantised out
     projection (:221). Returns a dict with the fp16 qkv, the fp16 context and the fp32 output;
     ``rows`` optionally restricts the context/output to a subset of flattened token rows.
     """
@@ -97,7 +108,9 @@ def int8_self_attention(x, params, num_heads: int, causal: bool = False, rows=No
     qkv16 = torch.from_numpy(qkv32.astype(np.float16))
     q5 = qkv16.float().view(B, S, 3, num_heads, hd)
     q, k, v = (q5[:, :, i].transpose(1, 2).contiguous() for i in range(3))
-    ctx = attention_core(q, k, v, hd ** -0.5, causal)              # fp32 math
+    # fp32 math; probabilities rounded to fp16 before P·V (p.to(tl.float16), k008:108; the
+    # eager branch's softmax(...).half(), :218)
+    ctx = attention_core(q, k, v, hd ** -0.5, causal, probs_dtype=torch.float16)
     ctx16 = ctx.transpose(1, 2).reshape(B * S, d).to(torch.float16)
     sel = ctx16 if rows is None else ctx16[rows]
     y, _ = int8_linear(sel.float().numpy(), pk["out_w"], pk["out_s"], pk["out_b"])
@@ -118,7 +131,8 @@ def int8_transformer_block(x, params, num_heads: int, valid_token_mask=None, cau
     """``block_forward`` of k008_int8_gemm.py:189-234 for an fp32 model, on CPU.
 
     norm1 (fp32, :195) -> int8 QKV -> fp16 qkv (:196-197) -> attention in fp32 math on the fp16
-    qkv with the key mask, context rounded to fp16 (:206-219) -> int8 out projection of the
+    qkv with the key mask, probabilities rounded to fp16 before P·V (:108, :218), context
+    rounded to fp16 (:206-219) -> int8 out projection of the
     context (:221) -> masked rows of it zeroed (:223-224) -> x + attn_out (:225) -> norm2
     (:227) -> int8 ffn_in (:228) -> exact GELU in fp32 (:229) -> int8 ffn_out (:230) ->
     x + out (:231) -> masked rows zeroed (:232-233). ``params`` uses the block's state-dict keys.
@@ -141,7 +155,8 @@ def int8_transformer_block(x, params, num_heads: int, valid_token_mask=None, cau
     qkv16 = torch.from_numpy(qkv32.astype(np.float16))
     q5 = qkv16.float().view(B, S, 3, num_heads, hd)
     q, k, v = (q5[:, :, i].transpose(1, 2).contiguous() for i in range(3))
-    ctx = attention_core(q, k, v, hd ** -0.5, causal, valid_token_mask)
+    ctx = attention_core(q, k, v, hd ** -0.5, causal, valid_token_mask,
+                         probs_dtype=torch.float16)               # P rounded (:108, :218)
     ctx16 = ctx.transpose(1, 2).reshape(T, d).to(torch.float16)
     attn_out = torch.from_numpy(int8_linear(ctx16.float().numpy(), pk["out_w"], pk["out_s"],
                                             pk["out_b"])[0])

@@ -107,6 +107,13 @@ def quant_case(name: str):
     rows.append(tie)
     rng = np.random.Generator(np.random.PCG64(7))
     rows += list(rng.standard_normal((11, K)) * rng.uniform(1e-3, 1e3, (11, 1)))
+    # non-finite rows: torch's amax/clamp propagate NaN into the scale (every code 0); an inf
+    # element makes the scale inf (its own code NaN -> 0, the finite ones round to 0)
+    nan_row = rng.standard_normal(K)
+    nan_row[3] = np.nan
+    inf_row = rng.standard_normal(K)
+    inf_row[5] = -np.inf
+    rows += [nan_row, inf_row]
     x = np.stack(rows).astype(np.float32)
     q0, s0 = OI.quant_rows(x)
     q1, s1 = OI.quant_weight(x)

@@ -156,3 +156,26 @@ def test_kernel_error_carries_status():
     with pytest.raises(L.KernelError) as ei:
         L.check("mi355_attn_fwd", -5)
     assert ei.value.status == -5 and "head_dim" in str(ei.value)
+
+
+def test_build_refuses_lds_dma_kernels_that_use_scratch():
+    """build.py parses the compiler's kernel-resource-usage remarks and refuses an LDS-DMA kernel
+    (attention MFMA / projection GEMM) that uses scratch memory or spills VGPRs."""
+    import importlib
+    B = importlib.import_module("tiktok_techjam_2026_track3_amd.build")
+    remarks = "\n".join([
+        "a.hip:1:1: remark: Function Name: _ZN12_GLOBAL__N_113attn_fwd_mfmaIDF16_Li64EEEvNS_8AttnArgsE [-R]",
+        "a.hip:1:1: remark:     ScratchSize [bytes/lane]: 16 [-R]",
+        "a.hip:1:1: remark:     SGPRs Spill: 0 [-R]",
+        "a.hip:1:1: remark:     VGPRs Spill: 4 [-R]",
+        "a.hip:2:1: remark: Function Name: _ZN12_GLOBAL__N_113attn_fwd_valuIfLi8EEEvNS_8AttnArgsE [-R]",
+        "a.hip:2:1: remark:     ScratchSize [bytes/lane]: 8 [-R]",
+        "a.hip:2:1: remark:     VGPRs Spill: 2 [-R]",
+    ])
+    usage = B.resource_usage(remarks)
+    assert usage["_ZN12_GLOBAL__N_113attn_fwd_mfmaIDF16_Li64EEEvNS_8AttnArgsE"] == {
+        "scratch": 16, "sgpr_spill": 0, "vgpr_spill": 4}
+    with pytest.raises(RuntimeError, match="must not use scratch"):
+        B.check_no_scratch("a.hip", usage)
+    # the vector-ALU kernel issues no LDS-DMA loads: not checked
+    B.check_no_scratch("a.hip", {k: v for k, v in usage.items() if "valu" in k})

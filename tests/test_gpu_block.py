@@ -20,6 +20,12 @@ from oracle import model as OM
 from oracle.predicate import compare_outputs
 from tiktok_techjam_2026_track3_amd import workloads as W
 
+import int8_requant
+
+# fraction of the C4 attention-half output elements that must pass the predicate against the
+# quantised recipe (the rest are bounded by their requantisation code moves)
+INT8_E2E_PASS_FLOOR = 0.95
+
 pytestmark = pytest.mark.gpu
 
 _rng = random.Random(int.from_bytes(os.urandom(4), "little"))
@@ -67,10 +73,12 @@ def test_int8_block_stages_match_quantised_recipe(gpu, seed):
     """C4 (W8A8). Every integer or rounded stage is compared bit for bit with the recipe
     (k008_int8_gemm.py:148-223): activation quantisation, the fp16 QKV after exact int32
     accumulation and dequantisation, and the out projection of the context. The attention stage
-    (fp16 probabilities, fp32 accumulation) is held to the predicate against fp32 math on the
-    same fp16 qkv. End to end, the recipe re-quantises the context per token to int8, which
-    turns fp16-ulp differences of the context into whole quantisation steps (about
-    s_ctx * s_w * |w_i8| ~ 5e-4 each) of the output; that distance is reported, not asserted.
+    (fp16 probabilities, fp32 accumulation) is held to the predicate against the recipe's own
+    attention on the same fp16 qkv. End to end, the recipe re-quantises the context per token,
+    so a context value next to a quantisation boundary can round to the neighbouring code:
+    every code may move by at most one step, every output element must stay within the bound
+    those code moves imply (tests/int8_requant.py), and at least INT8_E2E_PASS_FLOOR of the
+    elements must pass the predicate against the recipe.
     """
     from tiktok_techjam_2026_track3_amd import Int8SelfAttention
     w = W.CONFIGS["C4"].scaled(*REDUCED["C4"])
@@ -98,9 +106,11 @@ def test_int8_block_stages_match_quantised_recipe(gpu, seed):
     y_from_ours, _ = OI.int8_linear(keep["ctx"].reshape(T, d).float().cpu().numpy(),
                                     pk["out_w"], pk["out_s"], pk["out_b"])
     assert torch.equal(out.reshape(T, d).cpu(), torch.from_numpy(y_from_ours).to(torch.float16))
-    e2e = compare_outputs(want["out"], out.reshape(T, d))
+    frac, stats = int8_requant.check(keep["ctx"].reshape(T, d), want["ctx16"], pk["out_w"],
+                                     pk["out_s"], pk["out_b"], out.reshape(T, d))
+    print("end to end vs quantised recipe:", stats, flush=True)
+    assert frac >= INT8_E2E_PASS_FLOOR, stats
     ref32 = OA.self_attention(x.float(), params, w.heads, causal=w.causal)
-    print("reported: end to end vs quantised recipe:", e2e.summary(), flush=True)
     print("reported: end to end vs unquantised fp32 block:", compare_outputs(ref32, out).summary(),
           flush=True)
 

@@ -1,12 +1,15 @@
 """GPU parity at the full measured shapes.
 
-C2 is checked element by element against the dense CPU oracle. C3 and C5 are too large for a
-dense oracle (S x S scores of 34 GB / 10 TB), so sampled query rows (first, last, tile edges
+C2 is checked element by element against the dense CPU oracle, for the five fixed and two
+random seeds. C3 and C5 are too large for a dense oracle (S x S scores of 34 GB / 10 TB), so sampled query rows (first, last, tile edges
 and random) are checked against the streamed oracle (Project/tools/shape14_eval.py:201-236
 semantics) computed from the full keys/values of their batch row; in addition, the full-size
 call must equal per-batch-row calls bit for bit (the batch-decomposition property the
-reference checks in shape14_eval.py:674-750), and every output must be finite. C4 is checked
-stage by stage on sampled rows (bit-exact integer stages, predicate on attention).
+reference checks in shape14_eval.py:674-750), and every output must be finite; the other seeds
+check sampled rows of one batch row each. C5's attention core on its own inputs (Q, K, V ~
+N(0, 1) / 8) is checked on sampled rows for every seed. C4 is checked stage by stage on sampled
+rows (bit-exact integer stages, predicate on attention) and end to end within the requantisation
+bound.
 """
 import numpy as np
 import pytest
@@ -17,6 +20,9 @@ from oracle import int8 as OI
 from oracle import streamed as OS
 from oracle.predicate import compare_outputs
 from tiktok_techjam_2026_track3_amd import workloads as W
+
+import int8_requant
+from test_gpu_block import INT8_E2E_PASS_FLOOR, SEEDS
 
 pytestmark = pytest.mark.gpu
 
@@ -47,12 +53,13 @@ def _sampled_oracle(x_row, pf, w, idx):
     return torch.nn.functional.linear(ctx, pf["out_proj.weight"], pf["out_proj.bias"])
 
 
-def test_c2_full_dense(gpu):
+@pytest.mark.parametrize("seed", SEEDS)
+def test_c2_full_dense(gpu, seed):
     w = W.CONFIGS["C2"]
     params = W.round_params(W.make_params(w), w.dtype)
-    x = W.make_input(w, SEED)
+    x = W.make_input(w, seed)
     mod = _float_module(w, params, gpu)
-    print(f"C2 full B={w.batch} S={w.seq}", flush=True)
+    print(f"C2 full B={w.batch} S={w.seq} seed={seed}", flush=True)
     with torch.inference_mode():
         out = mod(x.to(gpu), torch.ones(w.batch, w.seq, dtype=torch.bool, device=gpu), w.causal)
     torch.set_num_threads(16)
@@ -83,6 +90,59 @@ def test_long_sequence_sampled_rows_and_decomposition(gpu, name):
             r = compare_outputs(ref[0], out[b, idx])
             print(f"{name} batch {b}: {len(idx)} sampled rows: {r.summary()}", flush=True)
             assert r.passed, r.summary()
+
+
+@pytest.mark.parametrize("seed", SEEDS[1:])
+@pytest.mark.parametrize("name", ["C3", "C5"])
+def test_long_sequence_more_seeds(gpu, name, seed):
+    """The other fixed and random seeds at full size: sampled rows of one batch row (a different
+    row per seed) against the streamed oracle."""
+    w = W.CONFIGS[name]
+    params = W.round_params(W.make_params(w), w.dtype)
+    pf = {k: v.float() for k, v in params.items()}
+    mod = _float_module(w, params, gpu)
+    x = W.make_input(w, seed, device="cuda")
+    b = seed % w.batch
+    print(f"{name} full seed={seed} batch row {b}", flush=True)
+    with torch.inference_mode():
+        out = mod(x, None, w.causal)
+    torch.cuda.synchronize()
+    torch.set_num_threads(16)
+    idx = _sample_rows(w.seq, 16, seed)
+    ref = _sampled_oracle(x[b:b + 1].cpu(), pf, w, idx)
+    r = compare_outputs(ref[0], out[b, idx])
+    print(f"{name} seed {seed} batch {b}: {r.summary()}", flush=True)
+    assert r.passed, r.summary()
+
+
+@pytest.mark.parametrize("scale", ["c5", "unscaled"])
+@pytest.mark.parametrize("seed", SEEDS)
+def test_c5_attention_core_sampled_rows(gpu, seed, scale):
+    """C5 as BASELINE states it: the streamed attention core on Q, K, V ~ N(0, 1) / sqrt(64)
+    (B32 S100000 H8 x 64, fp16), sampled query rows of two batch rows against the chunk-wise
+    oracle (shape14_eval.py:201-236) on the same rounded inputs; plus an unscaled N(0, 1)
+    variant, whose softmax is far from uniform (numerical coverage, one seed)."""
+    from tiktok_techjam_2026_track3_amd import ops
+    if scale == "unscaled" and seed != SEED:
+        pytest.skip("the unscaled variant runs on the first fixed seed only")
+    w = W.CONFIGS["C5"]
+    q, k, v = W.make_core_inputs(w, seed, device="cuda")
+    if scale == "unscaled":
+        q, k, v = ((t.float() * w.head_dim ** 0.5).to(w.dtype) for t in (q, k, v))
+    print(f"C5 core seed={seed} scale={scale}", flush=True)
+    with torch.inference_mode():
+        out = ops.attention(q, k, v)
+    torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    torch.set_num_threads(16)
+    for b in (seed % w.batch, (seed + 17) % w.batch):
+        idx = _sample_rows(w.seq, 16, seed + b)
+        qb, kb, vb = (t[b:b + 1].float().cpu().permute(0, 2, 1, 3) for t in (q, k, v))
+        ref = OS.streamed_attention_core(qb[:, :, idx], kb, vb, w.head_dim ** -0.5, False,
+                                         q_index=idx)
+        r = compare_outputs(ref[0].transpose(0, 1), out[b, idx])
+        print(f"C5 core batch {b}: {len(idx)} sampled rows: {r.summary()}", flush=True)
+        assert r.passed, r.summary()
 
 
 def test_c4_full_stagewise_sampled_rows(gpu):
@@ -126,3 +186,11 @@ def test_c4_full_stagewise_sampled_rows(gpu):
     y, _ = OI.int8_linear(keep["ctx"].view(T, d)[rows].float().cpu().numpy(),
                           pk["out_w"], pk["out_s"], pk["out_b"])
     assert torch.equal(out.reshape(T, d)[rows].cpu(), torch.from_numpy(y).to(torch.float16))
+    # end to end against the recipe on the sampled rows: its own attention (probabilities
+    # rounded to fp16, k008_int8_gemm.py:108, :218) on the same qkv, then its requantisation
+    ctx_rec = OA.attention_core(q, k, v, hd ** -0.5, False, probs_dtype=torch.float16)
+    ctx_rec = ctx_rec[0].transpose(0, 1).reshape(len(idx), d).to(torch.float16)
+    frac, stats = int8_requant.check(keep["ctx"].view(T, d)[rows], ctx_rec, pk["out_w"],
+                                     pk["out_s"], pk["out_b"], out.reshape(T, d)[rows])
+    print("C4 end to end vs the recipe (sampled rows):", stats, flush=True)
+    assert frac >= INT8_E2E_PASS_FLOOR, stats

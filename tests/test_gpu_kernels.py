@@ -202,19 +202,33 @@ def test_attention_other_head_dims(gpu, dtype, hd, causal, S):
     _attn_check(gpu, dtype, 2, 2, S, S, hd, causal, seed=hd + S)
 
 
-@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
-@pytest.mark.parametrize("hd", [8, 32, 256])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
+@pytest.mark.parametrize("hd", [8, 32, 64, 128, 256])
 @pytest.mark.parametrize("causal", [False, True])
 def test_attention_short_keys_many_tiles(gpu, dtype, hd, causal):
     """Up to 256 keys and at least 1024 query tiles: the vector-ALU kernel splits each tile's
     keys over 2 waves instead of 8 (B 48, H 8, S 100: 1536 to 4992 tiles), with and without a
-    key mask."""
+    key mask, and on packed q/k/v views (the strides the model passes). fp32 head dims 64 and
+    128 take this path in production (official shapes 9 and 10); 16-bit 64 / 128 run the MFMA
+    kernel at the same shapes."""
     B, S = 48, 100
     g = torch.Generator().manual_seed(hd + 7)
     mask = torch.rand(B, S, generator=g) > 0.2
     mask[:, 0] = True
     _attn_check(gpu, dtype, B, 8, S, S, hd, causal, seed=51)
     _attn_check(gpu, dtype, B, 8, S, S, hd, causal, key_valid=mask, seed=52)
+    _attn_check(gpu, dtype, B, 8, S, S, hd, causal, packed=True, seed=53)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("hd", [32, 64])
+@pytest.mark.parametrize("S", [256, 257])
+def test_attention_key_split_switch_point(gpu, dtype, hd, S):
+    """Both sides of the vector-ALU kernel's 2-wave / 8-wave key split (at most 256 keys and at
+    least 1024 query tiles take 2 waves): S = 256 and S = 257 with enough tiles."""
+    B = 64 if hd == 32 else 128
+    _attn_check(gpu, dtype, B, 4, S, S, hd, False, seed=S + hd)
+    _attn_check(gpu, dtype, B, 4, S, S, hd, True, seed=S + hd + 1)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])

@@ -345,6 +345,11 @@ def test_block_weight_updates_invalidate_ffn_cache(gpu):
 
 
 # ---------------------------------------------------------------------- int8 (W8A8) block
+# fraction of the whole int8 block's output elements that must pass the predicate against the
+# quantised recipe (fp32 model)
+INT8_BLOCK_PASS_FLOOR = 0.98
+
+
 def _round(a, dtype):
     return torch.from_numpy(np.asarray(a, dtype=np.float32)).to(dtype).float()
 
@@ -429,9 +434,15 @@ def test_int8_block_stages(gpu, dtype, causal):
     want[~valid] = 0
     assert torch.equal(y.reshape(T, d).float().cpu(), want)
     if dtype == torch.float32:
+        # end to end vs the recipe: four requantisation points (h, ctx, h2, gelu output) turn
+        # attention/LayerNorm rounding differences into int8 code moves; every stage above is
+        # exact or within the predicate given our own intermediates, and at least
+        # INT8_BLOCK_PASS_FLOOR of the output elements must pass the predicate end to end
         rec = OI.int8_transformer_block(x, p, H, mask, causal)["out"]
-        print("  reported: end to end vs the int8 recipe:", compare_outputs(rec, y.cpu()).summary(),
-              flush=True)
+        r = compare_outputs(rec, y.cpu())
+        frac = 1.0 - r.failed_elements / r.total_elements
+        print(f"  end to end vs the int8 recipe: pass fraction {frac:.5f}:", r.summary(), flush=True)
+        assert frac >= INT8_BLOCK_PASS_FLOOR, r.summary()
     flt = OB.transformer_block(x.float(), p, H, mask, causal)
     print("  reported: end to end vs the unquantised block:", compare_outputs(flt, y.cpu()).summary(),
           flush=True)

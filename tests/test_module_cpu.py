@@ -40,6 +40,31 @@ def test_graphed_forward_refuses_cpu_input():
         GraphedForward(mod, torch.zeros(1, 8, 64))
 
 
+def test_graphed_forward_refuses_replay_once_the_weight_cache_changed():
+    """The captured graph reads the module's packed weights by address: it holds the captured
+    cache entry (so the tensors stay alive) and refuses to replay once the module dropped or
+    rebuilt it -- a same-device .to() keeps every parameter's (data_ptr, version) but drops the
+    cache. (The object is assembled by hand: capture itself needs a GPU.)"""
+    from tiktok_techjam_2026_track3_amd import GraphedForward
+    mod = SelfAttention(64, 4)
+    gf = object.__new__(GraphedForward)
+    gf.module, gf.norm, gf.causal = mod, None, False
+    gf.static_x, gf.static_mask = torch.zeros(1, 8, 64), None
+    mod.__dict__["_mi355_pack"] = (("stamp",), ("packed weights",))
+    gf._stamp = gf._params_stamp()
+    gf._cache = mod.__dict__.get("_mi355_pack")
+    assert gf._cache_current()
+    mod.to(torch.float32)                      # same device and dtype: parameters untouched
+    assert gf._params_stamp() == gf._stamp     # the stamp alone would not notice
+    assert not gf._cache_current()
+    assert gf._cache == (("stamp",), ("packed weights",))   # the captured tensors stay referenced
+    with pytest.raises(RuntimeError, match="changed since capture"):
+        gf(torch.zeros(1, 8, 64))
+    mod.__dict__["_mi355_pack"] = (("stamp",), ("rebuilt",))  # a rebuilt cache is refused too
+    with pytest.raises(RuntimeError, match="changed since capture"):
+        gf(torch.zeros(1, 8, 64))
+
+
 def test_load_state_dict_and_apply_drop_derived_caches():
     mod = SelfAttention(32, 4)
     mod.__dict__["_mi355_pack"] = object()

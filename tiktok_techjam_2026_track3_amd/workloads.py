@@ -126,6 +126,24 @@ def make_input(w: Workload, seed: int, device: str = "cpu", input_scale: float =
     return x.to(w.dtype)
 
 
+def make_core_inputs(w: Workload, seed: int, device: str = "cpu"):
+    """The attention core's own inputs, as C5 states them: Q, K, V ~ N(0, 1) / sqrt(head_dim)
+    of shape [B, S, H, head_dim], drawn in fp32 (one seeded generator, Q then K then V) and
+    rounded to ``w.dtype``."""
+    g = torch.Generator(device=device)
+    g.manual_seed(seed)
+    shape = (w.batch, w.seq, w.heads, w.head_dim)
+    sc = 1.0 / math.sqrt(w.head_dim)
+    return tuple((torch.randn(shape, generator=g, device=device, dtype=torch.float32) * sc)
+                 .to(w.dtype) for _ in range(3))
+
+
+def core_flops_bytes(w: Workload):
+    """Algorithmic FLOPs and bytes of the attention core alone (Q, K, V read, O written once)."""
+    e = 2 if w.dtype in (torch.float16, torch.bfloat16) else 4
+    return w.flops()["attn"], 4.0 * w.tokens * w.d_model * e
+
+
 def round_params(params: Dict[str, torch.Tensor], dtype: torch.dtype) -> Dict[str, torch.Tensor]:
     """Parameters rounded to ``dtype`` (what a ``model.to(dtype)`` holds)."""
     return {k: v.to(dtype) for k, v in params.items()}
