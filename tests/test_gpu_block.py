@@ -23,8 +23,14 @@ from tiktok_techjam_2026_track3_amd import workloads as W
 import int8_requant
 
 # fraction of the C4 attention-half output elements that must pass the predicate against the
-# quantised recipe (the rest are bounded by their requantisation code moves)
-INT8_E2E_PASS_FLOOR = 0.95
+# quantised recipe (the rest are bounded by their requantisation code moves, which is asserted
+# per element). Measured 0.952-0.957 over seven seeds at the reduced shape (B1 S256 d4096):
+# about 1% of the requantised context codes move by one step (a context value one fp16 ulp from
+# the recipe's, next to a rounding boundary), every row has some, and each moved code shifts its
+# row's outputs by up to s_ctx*|w|*s_w. The floor sits below that spread, as a guard against a
+# context that drifts further from the recipe's; the full-size sampled rows and the golden case
+# measure 0.9998-1.0.
+INT8_E2E_PASS_FLOOR = 0.93
 
 pytestmark = pytest.mark.gpu
 
