@@ -10,11 +10,15 @@ reports with the commands that produced them):
 * ``traffic``     -- HBM bytes per launch of one kernel from a ``FETCH_SIZE`` run and a
   ``WRITE_SIZE`` run, each scaled by the factor that makes the same counter read exactly the
   known bytes of a plain copy kernel (``bench.py --copy-calibration``), written as JSON.
+* ``util DIR...`` -- per-kernel compute utilisation from one or more ``--pmc`` runs of the same
+  command (counters merged by kernel): MFMA busy, MFMA/VALU co-execution, VALU activity, the
+  shader clock, and the MFMA operation count, each with the formula it is computed by.
 
 Usage::
 
     python -m tiktok_techjam_2026_track3_amd.profiling stats gpurun_out/prof_C2
     python -m tiktok_techjam_2026_track3_amd.profiling pmc gpurun_out/fetch_C2
+    python -m tiktok_techjam_2026_track3_amd.profiling util gpurun_out/pmc1_C2 gpurun_out/pmc2_C2
     python -m tiktok_techjam_2026_track3_amd.profiling traffic --config C2 --kernel attn_fwd_mfma \\
         --fetch gpurun_out/fetch_C2 --write gpurun_out/write_C2 \\
         --copy-fetch gpurun_out/fetch_copy --copy-write gpurun_out/write_copy --copy-bytes N
@@ -82,20 +86,28 @@ def kernel_stats(d: str) -> List[dict]:
     return rows
 
 
+DURATION = "duration_ns"  # pseudo-counter: the dispatch's duration, when the CSV carries it
+
+
 def counters(d: str) -> Dict[str, Dict[str, List[float]]]:
-    """kernel name -> counter -> per-dispatch values (summed over dimensions of one dispatch)."""
+    """kernel name -> counter -> per-dispatch values (summed over dimensions of one dispatch);
+    ``DURATION`` holds each dispatch's duration when the rows carry start / end timestamps."""
     per = defaultdict(lambda: defaultdict(float))
-    names = {}
+    names, span = {}, {}
     for path in _find(d, "_counter_collection.csv"):
         with open(path, newline="") as f:
             for r in csv.DictReader(f):
                 key = (path, r["Dispatch_Id"])
                 names[key] = r["Kernel_Name"]
                 per[key][r["Counter_Name"]] += float(r["Counter_Value"])
+                if r.get("Start_Timestamp") and r.get("End_Timestamp"):
+                    span[key] = float(r["End_Timestamp"]) - float(r["Start_Timestamp"])
     out: Dict[str, Dict[str, List[float]]] = defaultdict(lambda: defaultdict(list))
     for key, vals in per.items():
         for c, v in vals.items():
             out[names[key]][c].append(v)
+        if key in span:
+            out[names[key]][DURATION].append(span[key])
     return out
 
 
@@ -127,6 +139,78 @@ def print_pmc(d: str) -> None:
         print(f"{short_name(name)} [{n} dispatches]: {vals}")
 
 
+# MI355X: 8 XCDs of 32 CUs, 4 SIMDs per CU; GRBM_GUI_ACTIVE is counted once per XCD
+N_XCD, N_CU, SIMD_PER_CU = 8, 256, 4
+UTIL_FORMULAS = """\
+  cycles      = GRBM_GUI_ACTIVE / 8                      (kernel cycles; the counter is per XCD)
+  clock GHz   = cycles / duration
+  MFMA busy   = SQ_VALU_MFMA_BUSY_CYCLES / (cycles * 1024 SIMDs)
+  co-exec     = SQ_VALU_MFMA_COEXEC_CYCLES / SQ_VALU_MFMA_BUSY_CYCLES
+                (share of MFMA-busy cycles in which a VALU instruction also issued)
+  VALU active = 4 * SQ_ACTIVE_INST_VALU / (cycles * 1024)  (wave-cycles on VALU instructions,
+                MFMA issue included, per SIMD-cycle; two resident waves can each count)
+  MFMA ops    = 512 * SQ_INSTS_VALU_MFMA_MOPS_{F16,BF16,I8}  (multiply-adds counted as 2)
+  MFMA rate   = MFMA ops / duration
+  wait        = SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES        (wave time waiting to issue)"""
+
+
+def utilisation(dirs: List[str]) -> List[dict]:
+    """Derived compute utilisation per kernel from one or more ``--pmc`` runs of one command."""
+    merged: Dict[str, Dict[str, List[float]]] = defaultdict(dict)
+    for d in dirs:
+        for name, cs in counters(d).items():
+            for c, v in cs.items():
+                if c == DURATION and c in merged[name]:
+                    merged[name][c] = merged[name][c] + v
+                else:
+                    merged[name][c] = v
+    rows = []
+    for name, cs in merged.items():
+        m = {c: _mean(v) for c, v in cs.items()}
+        cyc = m.get("GRBM_GUI_ACTIVE", 0.0) / N_XCD
+        simd_cycles = cyc * N_CU * SIMD_PER_CU
+        r = {"kernel": short_name(name),
+             "dispatches": max(len(v) for c, v in cs.items() if c != DURATION),
+             "cycles": cyc}
+        dur = m.get(DURATION)
+        if dur:
+            r["duration_us"] = dur / 1e3
+            r["clock_ghz"] = cyc / dur if cyc else None
+        if simd_cycles and "SQ_VALU_MFMA_BUSY_CYCLES" in m:
+            r["mfma_busy"] = m["SQ_VALU_MFMA_BUSY_CYCLES"] / simd_cycles
+            if "SQ_VALU_MFMA_COEXEC_CYCLES" in m and m["SQ_VALU_MFMA_BUSY_CYCLES"]:
+                r["coexec"] = m["SQ_VALU_MFMA_COEXEC_CYCLES"] / m["SQ_VALU_MFMA_BUSY_CYCLES"]
+        if simd_cycles and "SQ_ACTIVE_INST_VALU" in m:
+            r["valu_active"] = 4.0 * m["SQ_ACTIVE_INST_VALU"] / simd_cycles
+        ops = sum(m.get(f"SQ_INSTS_VALU_MFMA_MOPS_{t}", 0.0) for t in ("F16", "BF16", "I8")) * 512
+        if ops:
+            r["mfma_ops"] = ops
+            if dur:
+                r["mfma_tops"] = ops / dur / 1e3
+        if m.get("SQ_WAVE_CYCLES") and "SQ_WAIT_INST_ANY" in m:
+            r["wait"] = m["SQ_WAIT_INST_ANY"] / m["SQ_WAVE_CYCLES"]
+        for c in ("SQ_INSTS_VALU", "SQ_INSTS_MFMA", "SQ_INSTS_LDS", "SQ_LDS_BANK_CONFLICT"):
+            if c in m:
+                r[c] = m[c]
+        rows.append(r)
+    rows.sort(key=lambda r: -r["cycles"])
+    return rows
+
+
+def print_util(dirs: List[str]) -> None:
+    print(UTIL_FORMULAS)
+    print()
+    hdr = (f"{'kernel':44s} {'n':>3s} {'dur_us':>10s} {'GHz':>5s} {'MFMA':>6s} {'coex':>6s} "
+           f"{'VALU':>6s} {'wait':>6s} {'MFMA TOP/s':>10s} {'VALU inst':>11s} {'MFMA inst':>10s}")
+    print(hdr)
+    pct = lambda r, k: f"{100 * r[k]:5.1f}%" if r.get(k) is not None else "     -"
+    for r in utilisation(dirs)[:12]:
+        print(f"{r['kernel'][:44]:44s} {r['dispatches']:3d} {r.get('duration_us', 0):10.1f} "
+              f"{r.get('clock_ghz') or 0:5.2f} {pct(r, 'mfma_busy')} {pct(r, 'coexec')} "
+              f"{pct(r, 'valu_active')} {pct(r, 'wait')} {r.get('mfma_tops', 0):10.1f} "
+              f"{r.get('SQ_INSTS_VALU', 0):11.4g} {r.get('SQ_INSTS_MFMA', 0):10.4g}")
+
+
 def traffic(config: str, kernel: str, fetch: str, write: str, copy_fetch: str, copy_write: str,
             copy_bytes: float) -> dict:
     """HBM bytes per launch of ``kernel``; FETCH_SIZE / WRITE_SIZE are in KiB per dispatch."""
@@ -153,11 +237,15 @@ def main(argv=None) -> int:
         t.add_argument("--" + a, required=True)
     t.add_argument("--copy-bytes", type=float, required=True)
     t.add_argument("--json-out", help="merge the record into this JSON file (keyed by config)")
+    u = sub.add_parser("util")
+    u.add_argument("dirs", nargs="+")
     a = ap.parse_args(argv)
     if a.cmd == "stats":
         print_stats(a.dir)
     elif a.cmd == "pmc":
         print_pmc(a.dir)
+    elif a.cmd == "util":
+        print_util(a.dirs)
     else:
         rec = traffic(a.config, a.kernel, a.fetch, a.write, a.copy_fetch, a.copy_write, a.copy_bytes)
         print(json.dumps(rec, indent=1))
