@@ -12,7 +12,8 @@
 //   * probabilities are exp2(s*scale*log2e - m*scale*log2e) in fp32, rounded to the input dtype
 //     (the rounding point of torch_transformer_benchmark.py:111) and fed straight from registers
 //     as the B operand of O^T += V^T · P^T; each V^T fragment is built from the key-major V tile
-//     by two ds_read_b64_tr_b16 transpose reads;
+//     by two ds_read_b64_tr_b16 transpose reads; at head_dim 64 the fp16 row sums add the
+//     rounded probabilities of a sub-tile with packed fp16 adds and carry the total in fp32;
 //   * scores live in the log2 domain (Q pre-multiplied by scale*log2e) and every score MFMA chain
 //     starts from -mu, so exp2 consumes the MFMA output directly;
 //   * the running max mu is only moved when a tile's max exceeds it by more than 8, so the O/l
@@ -96,6 +97,14 @@ MI355_DEVINL int swz(int r) {
     return ((r & 1) << 1) ^ ((r & 2) << 1) ^ ((r >> 2) & 3);
 }
 
+// fp16 row sums per sub-tile (head_dim 64): 1 = a tree of packed fp16 adds over the rounded
+// probabilities (then fp32 across sub-tiles), 0 = fp32 adds of the unrounded ones. The tree is 30 instructions
+// per 64 probabilities against 62 (measured +1.5% at C5, +3% at C3); its partial sums stay exact
+// to 2^-11 per level (each probability is <= 2^8, a sub-tile's 32 per lane sum to <= 2^13).
+#ifndef MI355_ATTN_SUM16
+#define MI355_ATTN_SUM16 1
+#endif
+
 template <typename T>
 MI355_DEVINL typename Mfma<T>::frag pack8(const float* p) {
   typename Mfma<T>::frag f;
@@ -123,6 +132,24 @@ MI355_DEVINL float frag_sum(bf16x8 f, float acc) {
     acc = __builtin_amdgcn_fdot2_f32_bf16(pr, one, acc, false);
   }
   return acc;
+}
+
+// Sum of the fp16 probabilities of 4 fragments (32 per lane): a tree of packed fp16 adds, then the
+// two halves in fp32.
+MI355_DEVINL float prob_sum16(const f16x8 (&f)[4]) {
+  f16x2 r[16];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) r[4 * i + j] = f16x2{f[i][2 * j], f[i][2 * j + 1]};
+#pragma unroll
+  for (int i = 0; i < 8; ++i) r[i] = r[2 * i] + r[2 * i + 1];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) r[i] = r[2 * i] + r[2 * i + 1];
+#pragma unroll
+  for (int i = 0; i < 2; ++i) r[i] = r[2 * i] + r[2 * i + 1];
+  r[0] = r[0] + r[1];
+  return static_cast<float>(r[0][0]) + static_cast<float>(r[0][1]);
 }
 
 // QG query groups of 32 per wave: every K / V^T fragment read from LDS feeds QG MFMAs.
@@ -161,6 +188,9 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   constexpr int RB = 64 / KCH;
   constexpr int BLK = BN / RB;
   static_assert(BLK % NW == 0 || NW % BLK == 0, "loader shape");
+  // (head_dim 128 keeps fp32 sums: +0.6% there, and its context feeds the int8 re-quantisation
+  // of the W8A8 block, where a larger context error moves more int8 codes)
+  constexpr bool SUM16 = MI355_ATTN_SUM16 && __is_same(T, _Float16) && HD == 64;
 
   // LDS ring of NSTAGE stages x KT sub-tiles, K and V both in their natural [key][hd] layout.
   // Without the look-ahead a wave reads one stage while the other is in flight (double
@@ -231,7 +261,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
     koff[i] = static_cast<uint32_t>(row) * kstride + c * 16;
     voff[i] = static_cast<uint32_t>(row) * vstride + c * 16;
   }
-  auto issue_loads = [&](int j, int s, int k) {
+  auto issue_loads = [&](int j, int s, int k) MI355_LAMBDA_INLINE {
     const int k0 = j * BN;
     if constexpr (KMASK) {
       // the sub-tile's 64 mask bytes, one per lane, straight into LDS (keys past the end
@@ -292,7 +322,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   const int q_wave32 = static_cast<int>(q_wave);
   const float thr = 8.0f;  // log2 units: unnormalised probabilities stay <= 2^8
 
-  auto kfrag = [&](int st, int k, int t, int s) {
+  auto kfrag = [&](int st, int k, int t, int s) MI355_LAMBDA_INLINE {
     const int krow = 32 * t + l32, c = 2 * s + g;
     return __builtin_bit_cast(frag, k_lds[st][k][krow * KCH + (c ^ swz<KCH>(krow))]);
   };
@@ -312,7 +342,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
         v_off[half][mt] = row * ROWB + ((col / 8) ^ swz<KCH>(row)) * 16 + (col % 8) * 2;
       }
   }
-  auto vfrag = [&](int st, int k, int mt, int t, int hh) {
+  auto vfrag = [&](int st, int k, int mt, int t, int hh) MI355_LAMBDA_INLINE {
     typedef short s4 __attribute__((ext_vector_type(4)));
     typedef short s8 __attribute__((ext_vector_type(8)));
     const char* base = reinterpret_cast<const char*>(&v_lds[st][k][0]) + (32 * t + 16 * hh) * ROWB;
@@ -327,7 +357,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   auto active = [&](int j) { return !CAUSAL || j * BN <= q_wave32 + QW - 1; };
 
   // S^T of sub-tile j (log2 domain, minus mu): 64 keys x QW queries
-  auto score = [&](f32x16 (&sacc)[QG][2], const int st, const int k) {
+  auto score = [&](f32x16 (&sacc)[QG][2], const int st, const int k) MI355_LAMBDA_INLINE {
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
@@ -345,7 +375,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   };
 
   // masks and the lazy running max of sub-tile j; returns after any O/l/mu update
-  auto softmax_max = [&](f32x16 (&sacc)[QG][2], const int j, const int st, const int k) {
+  auto softmax_max = [&](f32x16 (&sacc)[QG][2], const int j, const int st, const int k) MI355_LAMBDA_INLINE {
     const int k0 = j * BN;
     // tile validity word: bit kk set <=> key k0 + kk is valid under the key mask
     uint64_t vbits = ~0ull;
@@ -412,11 +442,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   };
 
   // probabilities of sub-tile j and O^T (hd x QW) += V^T (hd x 64 keys) . P^T (64 keys x QW)
-  auto exp_pv = [&](f32x16 (&sacc)[QG][2], const int st, const int k) {
-    frag pf[QG][2][2];
+  // probabilities of a sub-tile (rounded to T: the rounding point of :111) and their row sums
+  auto make_probs = [&](f32x16 (&sacc)[QG][2], frag (&pf)[QG][2][2], float (&part)[QG]) MI355_LAMBDA_INLINE {
 #pragma unroll
     for (int n = 0; n < QG; ++n) {
-      float part[4];
+      float pp[4];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
         float pv[16];
@@ -424,21 +454,30 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
         for (int i = 0; i < 16; ++i) pv[i] = fast_exp2(sacc[n][t][i]);
         pf[n][t][0] = pack8<T>(pv);
         pf[n][t][1] = pack8<T>(pv + 8);
-        if constexpr (!CAUSAL) {
+        if constexpr (!SUM16 && !CAUSAL) {
           // row sums in fp32 adds of the unrounded probabilities: v_dot2 on the packed values
           // halves the instruction count but cannot issue while another wave's MFMA runs
-          part[2 * t] = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
-          part[2 * t + 1] =
+          pp[2 * t] = ((pv[0] + pv[1]) + (pv[2] + pv[3])) + ((pv[4] + pv[5]) + (pv[6] + pv[7]));
+          pp[2 * t + 1] =
               ((pv[8] + pv[9]) + (pv[10] + pv[11])) + ((pv[12] + pv[13]) + (pv[14] + pv[15]));
-        } else {
+        } else if constexpr (!SUM16) {
           // the causal instances have no registers to spare for the fp32 sums (they would
           // spill): v_dot2 on the packed values
-          part[2 * t] = frag_sum(pf[n][t][0], 0.f);
-          part[2 * t + 1] = frag_sum(pf[n][t][1], 0.f);
+          pp[2 * t] = frag_sum(pf[n][t][0], 0.f);
+          pp[2 * t + 1] = frag_sum(pf[n][t][1], 0.f);
         }
       }
-      lsum[n] += (part[0] + part[1]) + (part[2] + part[3]);
+      if constexpr (SUM16) {
+        const frag fl[4] = {pf[n][0][0], pf[n][0][1], pf[n][1][0], pf[n][1][1]};
+        part[n] = prob_sum16(fl);
+      } else {
+        part[n] = (pp[0] + pp[1]) + (pp[2] + pp[3]);
+      }
     }
+  };
+
+  // O^T (hd x QW) += V^T (hd x 64 keys) . P^T (64 keys x QW)
+  auto pv_mma = [&](const frag (&pf)[QG][2][2], const int st, const int k) MI355_LAMBDA_INLINE {
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int mt = 0; mt < MT; ++mt) {
@@ -457,8 +496,18 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
   };
 
+  // probabilities of sub-tile j after softmax_max, and the P.V update
+  auto exp_pv = [&](f32x16 (&sacc)[QG][2], const int st, const int k) MI355_LAMBDA_INLINE {
+    frag pf[QG][2][2];
+    float part[QG];
+    make_probs(sacc, pf, part);
+#pragma unroll
+    for (int n = 0; n < QG; ++n) lsum[n] += part[n];
+    pv_mma(pf, st, k);
+  };
+
   // S^T of a sub-tile from K fragments already in registers
-  auto score_regs = [&](f32x16 (&sacc)[QG][2], const frag (&kf)[2][KS]) {
+  auto score_regs = [&](f32x16 (&sacc)[QG][2], const frag (&kf)[2][KS]) MI355_LAMBDA_INLINE {
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int t = 0; t < 2; ++t)
@@ -481,7 +530,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   // barrier. (cur, nxt, far: ring slots of this stage, the next one and the one being filled;
   // par: parity of its first sub-tile, which selects the score buffer; all are literals after
   // unrolling)
-  auto stage = [&](const int st, const int cur, const int nxt, const int far, const int par) {
+  auto stage = [&](const int st, const int cur, const int nxt, const int far, const int par) MI355_LAMBDA_INLINE {
 #pragma unroll
     for (int k = 0; k < KT; ++k) {
       const int j = st * KT + k, jf = j + (NSTAGE - 1) * KT;

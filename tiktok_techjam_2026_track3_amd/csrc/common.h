@@ -20,6 +20,9 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
 
 #define MI355_DEVINL __device__ __forceinline__
+// for lambdas inside kernels: a lambda left out of line takes its by-reference register arrays
+// through scratch memory
+#define MI355_LAMBDA_INLINE __attribute__((always_inline))
 
 // Per-element-type traits for the 32x32 MFMA family used by every kernel here.
 //   vec8  : one 16-byte MFMA operand fragment (8 x 16-bit, 16 x int8 packed in u32x4, 4 x fp32)
@@ -168,3 +171,11 @@ MI355_DEVINL void buffer_load_lds16(const void* base, uint32_t bytes, void* lds_
 }
 
 inline bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+
+// Row statistics pass (csrc/layernorm.hip): stats[2 m] = mean, stats[2 m + 1] = 1 / sqrt(var + eps)
+// of row m of X [M, K] (dtype MI355_F32 / F16 / BF16). Library-internal; arguments are checked by
+// the exported entry point that calls it.
+__attribute__((visibility("hidden"))) int mi355_internal_ln_stats(int dtype, const void* X,
+                                                                  int64_t ldx, float eps,
+                                                                  float* stats, int64_t M,
+                                                                  int64_t K, hipStream_t s);
