@@ -68,6 +68,9 @@ def parse_args():
                          "on the kernels: norm1, QKV, attention, out + residual, norm2, ffn_in + "
                          "GELU, ffn_out + residual + row mask; ffn_dim = 4 d_model (16-bit / fp32 "
                          "configurations)")
+    ap.add_argument("--unfolded", action="store_true",
+                    help="with --attention-half / --full-block: run the LayerNorms as their own "
+                         "row kernels instead of folding them into the QKV / ffn_in projections")
     ap.add_argument("--graph", action="store_true",
                     help="time replays of one step captured in a HIP graph (torch.cuda.CUDAGraph): "
                          "no per-kernel host launch cost; the per-stage breakdown still comes from "
@@ -288,13 +291,17 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
                       "ffn_in", "quant_g", "ffn_out"]
         else:
             blk = blk.to(device=dev, dtype=w.dtype).eval()
-            stages = ["norm", "qkv", "attn", "out", "norm2", "ffn_in", "ffn_out"]
+            # folded LayerNorms run inside the "qkv" / "ffn_in" stages (statistics pass included)
+            fold = blk.attention.folds_norm(w.dtype)
+            stages = ([] if fold else ["norm"]) + ["qkv", "attn", "out"] + \
+                ([] if fold else ["norm2"]) + ["ffn_in", "ffn_out"]
 
         def step(marks=None):
             return block_forward(blk, x, valid, w.causal, marks=marks)
     elif half:
         norm = torch.nn.LayerNorm(w.d_model).to(device=dev, dtype=w.dtype)
-        stages = ["norm"] + stages
+        if w.int8 or not mod.folds_norm(w.dtype):
+            stages = ["norm"] + stages
 
         def step(marks=None):
             return mod.forward_residual(x, norm, valid, w.causal, marks=marks)
@@ -402,20 +409,26 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         by = {"attn": cb}
     if half or full:
         act = w.tokens * w.d_model * x.element_size()
-        by["norm"] = 2 * act                      # read x, write norm1(x)
+        if "norm" in stages:
+            by["norm"] = 2 * act                  # read x, write norm1(x)
+        else:
+            by["qkv"] = by["qkv"] + act + 8 * w.tokens  # the statistics pass: read x, write stats
         by["out"] = by["out"] + act               # the residual read in the epilogue
     if full:
         e = x.element_size()
         T, d = w.tokens, w.d_model
         fl["ffn_in"] = 2.0 * T * d * ffn_dim
         fl["ffn_out"] = 2.0 * T * ffn_dim * d
-        by["norm2"] = 2 * act
+        if "norm2" in stages:
+            by["norm2"] = 2 * act
         if w.int8:
             # int8 operands and their fp32 scales in, activation-dtype outputs (+ residual read)
             by["ffn_in"] = T * d + ffn_dim * d + 4 * (T + ffn_dim) + 4 * ffn_dim + T * ffn_dim * e
             by["ffn_out"] = T * ffn_dim + d * ffn_dim + 4 * (T + d) + 4 * d + 2 * T * d * e
         else:
             by["ffn_in"] = (T * d + ffn_dim * d) * e + 4 * ffn_dim + T * ffn_dim * e
+            if "norm2" not in stages:
+                by["ffn_in"] += T * d * e + 8 * T     # the statistics pass over x1
             by["ffn_out"] = (T * ffn_dim + d * ffn_dim) * e + 4 * d + 2 * T * d * e
     stage_ms = {}
     for i, s in enumerate(stages):
@@ -597,6 +610,10 @@ def main() -> int:
         print(json.dumps(copy_calibration(args.copy_calibration)), flush=True)
         return 0
     from tiktok_techjam_2026_track3_amd import workloads as W
+    from tiktok_techjam_2026_track3_amd import SelfAttention
+
+    if args.unfolded:
+        SelfAttention.fold_norm = False
 
     if args.official:
         ids = (sorted(W.OFFICIAL_SHAPES) if args.official == "all"
@@ -628,6 +645,10 @@ def main() -> int:
         log(f"[bench] {token} ({mode}): warmup {warmup}, steps {steps} in {args.rounds} rounds")
         res = measure(name, steps, warmup, args.min_warmup_s, mode == "half", args.graph,
                       mode == "full", mode == "core", args.rounds)
+        if mode in ("half", "full"):
+            res["config"]["layernorm"] = (
+                "folded into the projections" if (SelfAttention(8, 1).folds_norm(W.CONFIGS[name].dtype)
+                                                  and not W.CONFIGS[name].int8) else "own row kernels")
         log(f"[bench] {token}: {res['ms_per_step']} ms/step (median), {res['value']} {res['unit']}, "
             f"roofline {res['roofline']['kernel']} {res['roofline']['frac']}")
         if not args.no_cpu_baseline:

@@ -196,6 +196,31 @@ int mi355_layernorm_masked(int dtype, const void* X, int64_t ldx, const void* ga
                            float eps, void* Y, int64_t ldy, int64_t M, int64_t K,
                            const uint8_t* row_valid, void* stream);
 
+/*
+ * LayerNorm folded into a projection:
+ *   C = out_dtype( LayerNorm(X) · W^T + b )   with LayerNorm(X) = (X - mean) * rstd * gamma + beta
+ * Replaces `self.norm1(x)` feeding the packed QKV projection (torch_transformer_benchmark.py:139,
+ * :93-95) -- the reference's fused LN-prologue QKV kernels `nq_launch(cfg, X, W, Bias, LnW, LnB,
+ * Out, tokens, D)` (Project/kernels/k024_cuda_tuned.py:201-234) and `_sub_norm_qkv`
+ * (Project/submission/dispatcher_region.py:343-399) -- and, with epi = MI355_EPI_GELU,
+ * `F.gelu(self.ffn_in(self.norm2(x)))` (:141). The normalised rows are never written: the caller
+ * passes the folded weight Wf[n, k] = W[n, k] * gamma[k] (rounded to in_dtype, row stride ldw),
+ * colsum[n] = sum_k Wf[n, k] (fp32) and bias[n] = b[n] + sum_k beta[k] W[n, k] (fp32, NULL = 0);
+ * one pass computes each row's mean and rstd = 1 / sqrt(var + eps) (biased variance, fp32; 0 for a
+ * row of equal elements, whose normalised values are exactly beta) into `stats` (caller workspace
+ * of 2 * M floats, 8-byte aligned, overwritten), and the projection of the raw X forms
+ * rstd * (X·Wf^T - mean * colsum) + bias in its epilogue (then the exact GELU of that value
+ * rounded to out_dtype, with MI355_EPI_GELU). X·Wf^T accumulates in fp32, so a row whose mean is
+ * large against its spread (|mean| * rstd >> 1) carries an extra error of about
+ * rstd * |mean| * sum_k |Wf[n, k]| * K / 16 * 2^-24. out_dtype is in_dtype, or F16 for a BF16
+ * input (the attention core type of a bf16 model). Requirements as mi355_gemm_bias, and
+ * K / (16 / sizeof(elem)) <= 1024.
+ */
+int mi355_layernorm_gemm_bias(int in_dtype, int out_dtype, const void* X, int64_t ldx,
+                              const void* W, int64_t ldw, const float* colsum, const float* bias,
+                              float eps, float* stats, void* C, int64_t ldc, int64_t M, int64_t N,
+                              int64_t K, int epi, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

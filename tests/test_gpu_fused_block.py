@@ -15,6 +15,7 @@ Bars:
   the reference itself rounds that output to bf16 before the residual add and any difference
   in the attention output can move that rounding by one step.
 """
+import math
 import os
 import random
 
@@ -35,6 +36,12 @@ print(f"random seeds for this run: {RANDOM_SEEDS}", flush=True)
 SEEDS = W.FIXED_SEEDS + RANDOM_SEEDS
 
 MANT = {torch.float16: 10, torch.bfloat16: 7, torch.float32: 23}
+UNIT_OF = {torch.float16: 2.0 ** -11, torch.bfloat16: 2.0 ** -8, torch.float32: 2.0 ** -24}
+
+
+def OA_gelu(y: torch.Tensor) -> torch.Tensor:
+    """Exact (erf) GELU in fp64."""
+    return 0.5 * y * (1.0 + torch.erf(y / math.sqrt(2.0)))
 
 
 def _ulp(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
@@ -148,18 +155,121 @@ def _half_case(name, seed, gpu, masked):
 @pytest.mark.parametrize("masked", [False, True])
 @pytest.mark.parametrize("name", ["C1", "C2", "C3"])
 def test_attention_half_is_the_unfused_composition(gpu, name, masked):
-    """forward_residual == x + forward(layer_norm(x)) bit for bit: the fusion changes no value."""
+    """With the LayerNorm kernel (fold_norm off), forward_residual == x + forward(layer_norm(x))
+    bit for bit: fusing the residual add changes no value. With the fold (the default) the
+    masked rows still keep x exactly and the output stays within the predicate of the unfused
+    composition (both are judged against the oracle in test_attention_half_matches_oracle)."""
     from tiktok_techjam_2026_track3_amd import ops
     w, params, x, norm, _, valid, mod = _half_case(name, 1234, gpu, masked)
     xg = x.to(gpu)
     vg = None if valid is None else valid.to(gpu)
     with torch.inference_mode():
+        mod.fold_norm = False
         fused = mod.forward_residual(xg, norm, vg, w.causal)
+        del mod.fold_norm
         h = ops.layer_norm(xg.reshape(-1, w.d_model), norm.weight, norm.bias, norm.eps)
         comp = xg + mod(h.view_as(xg), vg, w.causal)
+        folded = mod.forward_residual(xg, norm, vg, w.causal)
     assert torch.equal(fused, comp)
+    r = compare_outputs(comp.float().cpu(), folded.cpu())
+    print(f"folded vs unfused half {name}: {r.summary()}", flush=True)
+    if w.dtype == torch.bfloat16:
+        # bf16 keeps the LayerNorm kernel (SelfAttention.folds_norm): the same computation
+        assert not mod.folds_norm(w.dtype)
+        assert torch.equal(folded, comp)
+    else:
+        assert r.passed, r.summary()
     if valid is not None:
         assert torch.equal(fused[~vg], xg[~vg])
+        assert torch.equal(folded[~vg], xg[~vg])
+
+
+# ------------------------------------------------- LayerNorm folded into the projection GEMM
+LNF_TYPES = [(torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16),
+             (torch.bfloat16, torch.float16), (torch.float32, torch.float32)]
+
+
+def _lnf_inputs(M, K, N, dtype, seed):
+    g = torch.Generator().manual_seed(seed)
+    x = torch.randn(M, K, generator=g)
+    x[1::7] += 30.0                               # rows with a large mean (cancellation)
+    x[2] = 0.0                                    # zero row (the harness's padding)
+    x[3] = 2.5                                    # constant row: normalised values are beta
+    x[4] = torch.randn(K, generator=g) * 1e-3     # small spread: rstd near 1/sqrt(var)
+    x = x.to(dtype)
+    gamma = (1 + 0.3 * torch.randn(K, generator=g)).to(dtype)
+    beta = (0.2 * torch.randn(K, generator=g)).to(dtype)
+    w = (torch.randn(N, K, generator=g) / math.sqrt(K)).to(dtype)
+    b = (0.1 * torch.randn(N, generator=g)).to(dtype)
+    return x, gamma, beta, w, b
+
+
+@pytest.mark.parametrize("dtype,odt", LNF_TYPES)
+@pytest.mark.parametrize("M,N,K", [(300, 768, 256), (1000, 3072, 1024), (96, 64, 32), (130, 200, 128)])
+@pytest.mark.parametrize("gelu", [False, True])
+def test_layernorm_linear_error_bound(gpu, dtype, odt, M, N, K, gelu):
+    """ops.layernorm_linear (row statistics + projection of the raw x with gamma folded into
+    the weights, mean / rstd / beta in the epilogue) against fp64 LayerNorm -> nn.Linear (->
+    GELU) of the same rounded inputs, within a bound built from its rounding points: the folded
+    weights rounded to the operand type, fp32 accumulation (which the mean subtraction turns into
+    an error relative to |x|, not to |x - mean|), the statistics in fp32, and the output
+    rounding; plus the benchmark's predicate. Rows: random, large-mean, zero, constant and
+    small-spread ones; K = 32 takes the register-staged loader, the others the LDS-DMA one."""
+    from tiktok_techjam_2026_track3_amd import ops
+    print(f"layernorm_linear {dtype}->{odt} M={M} N={N} K={K} gelu={gelu}", flush=True)
+    x, gamma, beta, w, b = _lnf_inputs(M, K, N, dtype, seed=M + N + K)
+    wf, colsum, bf = ops.fold_layernorm(w.to(gpu), b.to(gpu), gamma.to(gpu), beta.to(gpu), dtype)
+    stats = torch.empty(M, 2, device=gpu)
+    out = ops.layernorm_linear(x.to(gpu), wf, colsum, bf, 1e-5, out_dtype=odt, gelu=gelu,
+                               stats=stats).cpu().double()
+    x64, g64, be64, w64 = x.double(), gamma.double(), beta.double(), w.double()
+    mu = x64.mean(dim=1, keepdim=True)
+    var = ((x64 - mu) ** 2).mean(dim=1, keepdim=True)
+    r = 1.0 / torch.sqrt(var + 1e-5)
+    y = ((x64 - mu) * r * g64 + be64) @ w64.T + b.double()
+    # statistics: fp32 sums of K terms; a constant row reports rstd 0 (its term is exactly 0)
+    st = stats.cpu().double()
+    assert torch.allclose(st[:, 0:1], mu, rtol=0, atol=1e-6 * (1 + mu.abs().max().item()) * K / 64)
+    const = var.squeeze(1) == 0
+    assert torch.all(st[const, 1] == 0)
+    assert torch.allclose(st[~const, 1:2], r[~const], rtol=K * 2.0 ** -22, atol=0)
+    u_in = UNIT_OF[dtype]
+    wf64 = wf.cpu().double()
+    bound = r * (u_in * ((x64 - mu).abs() @ (g64[None, :] * w64).abs().T)
+                 + K * 2.0 ** -24 * (x64.abs() @ wf64.abs().T + mu.abs() * wf64.abs().sum(1)[None, :]))
+    bound = bound + K * 2.0 ** -22 * y.abs() + 1e-6
+    if gelu:
+        want = OA_gelu(y)
+        bound = 1.13 * (bound + UNIT_OF[odt] * y.abs()) + 2e-6 * y.abs() + UNIT_OF[odt] * want.abs() + 1e-6
+    else:
+        want = y
+        bound = bound + UNIT_OF[odt] * y.abs()
+    err = (out - want).abs()
+    worst = float((err / bound).max())
+    print(f"  max_err={float(err.max()):.3g} worst err/bound={worst:.3f}", flush=True)
+    assert worst <= 1.0
+    if dtype != torch.bfloat16:
+        rep = compare_outputs(want.float(), out.float())
+        print("  predicate:", rep.summary(), flush=True)
+        assert rep.passed, rep.summary()
+    # the constant and zero rows: exactly the bias term rounded (no rstd amplification)
+    for row in (2, 3):
+        assert float(err[row].max()) <= float(bound[row].max())
+
+
+def test_layernorm_linear_rejects_bad_arguments(gpu):
+    from tiktok_techjam_2026_track3_amd import ops, _lib
+    x = torch.randn(8, 64, device=gpu, dtype=torch.float16)
+    w = torch.randn(32, 64, device=gpu, dtype=torch.float16)
+    cs, b = torch.zeros(32, device=gpu), torch.zeros(32, device=gpu)
+    with pytest.raises(ValueError):
+        ops.layernorm_linear(x, w, cs[:16], b)
+    with pytest.raises(ValueError):
+        ops.layernorm_linear(x, w.float(), cs, b)
+    with pytest.raises(_lib.KernelError):
+        ops.layernorm_linear(x, w, cs, b, out_dtype=torch.bfloat16)   # fp16 in, bf16 out
+    with pytest.raises(_lib.KernelError):
+        ops.layernorm_linear(x[:, :60], w[:, :60].contiguous(), cs, b)   # K not a multiple of 8
 
 
 @pytest.mark.parametrize("seed", SEEDS)

@@ -65,14 +65,39 @@ def test_graphed_forward_refuses_replay_once_the_weight_cache_changed():
         gf(torch.zeros(1, 8, 64))
 
 
+def test_graphed_forward_refuses_replay_once_the_folded_norm_weights_changed():
+    """The attention half's graph also reads the LayerNorm-folded QKV weights by address: a
+    dropped or rebuilt fold (e.g. after norm1's parameters changed) refuses replay too."""
+    from tiktok_techjam_2026_track3_amd import GraphedForward
+    mod = SelfAttention(64, 4)
+    norm = torch.nn.LayerNorm(64)
+    gf = object.__new__(GraphedForward)
+    gf.module, gf.norm, gf.causal = mod, norm, False
+    gf.static_x, gf.static_mask = torch.zeros(1, 8, 64), None
+    mod.__dict__["_mi355_pack"] = (("stamp",), ("packed weights",))
+    mod.__dict__["_mi355_lnpack"] = (("ln stamp",), ("folded weights",))
+    gf._stamp = gf._params_stamp()
+    gf._cache = mod.__dict__.get("_mi355_pack")
+    gf._ln_cache = mod.__dict__.get("_mi355_lnpack")
+    assert gf._cache_current()
+    mod.__dict__["_mi355_lnpack"] = (("ln stamp 2",), ("refolded",))
+    assert not gf._cache_current()
+    with pytest.raises(RuntimeError, match="changed since capture"):
+        gf(torch.zeros(1, 8, 64))
+    with torch.no_grad():
+        norm.weight.add_(1.0)                  # the norm's parameters are in the stamp
+    assert gf._params_stamp() != gf._stamp
+
+
 def test_load_state_dict_and_apply_drop_derived_caches():
     mod = SelfAttention(32, 4)
-    mod.__dict__["_mi355_pack"] = object()
-    mod.load_state_dict(mod.state_dict(), strict=True)
-    assert "_mi355_pack" not in mod.__dict__
-    mod.__dict__["_mi355_pack"] = object()
-    mod.half()
-    assert "_mi355_pack" not in mod.__dict__
+    for key in ("_mi355_pack", "_mi355_lnpack"):
+        mod.__dict__[key] = object()
+        mod.load_state_dict(mod.state_dict(), strict=True)
+        assert key not in mod.__dict__
+        mod.__dict__[key] = object()
+        mod.half()
+        assert key not in mod.__dict__
 
 
 def test_param_stamp_tracks_in_place_updates():

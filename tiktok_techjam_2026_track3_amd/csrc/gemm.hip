@@ -38,6 +38,8 @@ struct GemmArgs {
   const float* s_w;  // int8 only
   const uint8_t* row_valid;
   const void* R;  // residual [M, N] of the output dtype, nullable: C = R + round(A W^T + b)
+  const float* ln_stats;   // LayerNorm fold: per row (mean, rstd) [M][2] (LNF instances only)
+  const float* ln_colsum;  // LayerNorm fold: per column sum_k W[n, k] of the folded weight
   int64_t lda, ldw, ldc, ldr;
   int64_t M, N, K;
   int out_dtype;
@@ -52,6 +54,18 @@ struct GemmArgs {
 //                    add instead of as the residual (the block's trailing masked_fill).
 constexpr int EPI_GELU = 1;
 constexpr int EPI_ZERO_MASKED = 2;
+
+// LayerNorm folded into the projection (compile-time variant LNF, mi355_layernorm_gemm_bias):
+// A is the raw input x, W the weight with gamma folded in (W'[n, k] = W[n, k] gamma[k], rounded
+// to the operand dtype), bias' = b + W beta, colsum[n] = sum_k W'[n, k]; with the row statistics
+// (mean, rstd) of x the epilogue forms
+//     y = rstd * (x W'^T - mean colsum) + bias' = ((x - mean) rstd gamma + beta) W^T + b,
+// two FMAs per element. x W'^T accumulates exact products of the operands in fp32 and
+// subtracting mean * colsum removes the row mean from the same rounded weights, so no
+// cancellation beyond fp32 accumulation error is introduced.
+MI355_DEVINL float ln_fold(float acc, float mean, float rstd, float colsum, float bias) {
+  return __builtin_fmaf(rstd, __builtin_fmaf(-mean, colsum, acc), bias);
+}
 
 // Exact GELU, x * Phi(x) with Phi(x) = erfc(-x / sqrt 2) / 2, in fp32. erfc comes from the
 // Chebyshev fit of Numerical Recipes (Press et al., "erfcc"; fractional error below 1.2e-7 for
@@ -133,7 +147,8 @@ MI355_DEVINL void tile_coords(int64_t pid, int64_t ntm, int64_t ntn, int64_t& tm
 // M0 + 16*lane), so no registers or ds_write instructions carry the tiles, into a ring of NST
 // slots of CHK chunks per row. Requires K % BK == 0. Otherwise a register-staged, double-
 // buffered loader with bounds checks runs (8 chunks per row).
-template <typename T, typename TO, int BM, int BN, int WM, int WN, bool INT8, bool DIRECT, bool GELU>
+template <typename T, typename TO, int BM, int BN, int WM, int WN, bool INT8, bool DIRECT, bool GELU,
+          bool LNF>
 __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) void gemm_kernel(GemmArgs p) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
@@ -399,38 +414,74 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
   }
 
   // ---- epilogue: per element bias / dequantisation / row mask, rounded once to TO
+  // Per-row values (row mask, int8 activation scale, LayerNorm statistics) are read once per row;
+  // per-column values (bias, int8 weight scale, folded-LayerNorm column sums) once per group of
+  // 4 consecutive features, as one 16-byte load when the group is inside N and the arrays are
+  // 16-byte aligned, and shared by the TM row blocks.
   char* cl = reinterpret_cast<char*>(lds_raw);
+  bool in_m_[TM], valid_[TM];
+  float sa_m[TM], mean_m[TM], rstd_m[TM];
 #pragma unroll
   for (int a = 0; a < TM; ++a) {
-    const int m_loc = wm * WTM + a * 32 + l32;
-    const int64_t m = m0 + m_loc;
-    const bool in_m = m < p.M;
-    const bool valid = !in_m || p.row_valid == nullptr || p.row_valid[m] != 0;
-    float sa_m = 0.f;
-    if constexpr (INT8) sa_m = in_m ? p.s_a[m] : 0.f;
+    const int64_t m = m0 + wm * WTM + a * 32 + l32;
+    in_m_[a] = m < p.M;
+    valid_[a] = !in_m_[a] || p.row_valid == nullptr || p.row_valid[m] != 0;
+    sa_m[a] = 0.f;
+    if constexpr (INT8) sa_m[a] = in_m_[a] ? p.s_a[m] : 0.f;
+    mean_m[a] = 0.f;
+    rstd_m[a] = 0.f;
+    if constexpr (LNF) {
+      if (in_m_[a]) {
+        mean_m[a] = p.ln_stats[2 * m];
+        rstd_m[a] = p.ln_stats[2 * m + 1];
+      }
+    }
+  }
+  const bool col_vec = ((reinterpret_cast<uintptr_t>(p.bias) | reinterpret_cast<uintptr_t>(p.s_w) |
+                         reinterpret_cast<uintptr_t>(p.ln_colsum)) & 15u) == 0;
+  auto col4 = [&](const float* arr, int64_t nb) MI355_LAMBDA_INLINE {
+    f32x4 r = {0.f, 0.f, 0.f, 0.f};
+    if (arr == nullptr) return r;
+    if (col_vec && nb + 3 < p.N) return *reinterpret_cast<const f32x4*>(arr + nb);
 #pragma unroll
-    for (int b = 0; b < TN; ++b) {
+    for (int e = 0; e < 4; ++e)
+      if (nb + e < p.N) r[e] = arr[nb + e];
+    return r;
+  };
 #pragma unroll
-      for (int i4 = 0; i4 < 4; ++i4) {
-        const int n_loc = wn * WTN + b * 32 + 8 * i4 + 4 * g;  // 4 consecutive features
+  for (int b = 0; b < TN; ++b) {
+#pragma unroll
+    for (int i4 = 0; i4 < 4; ++i4) {
+      const int n_loc = wn * WTN + b * 32 + 8 * i4 + 4 * g;  // 4 consecutive features
+      const int64_t nb = n0 + n_loc;
+      const f32x4 bias4 = col4(p.bias, nb);
+      const f32x4 sw4 = INT8 ? col4(p.s_w, nb) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const f32x4 cs4 = LNF ? col4(p.ln_colsum, nb) : f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int a = 0; a < TM; ++a) {
+        const int m_loc = wm * WTM + a * 32 + l32;
+        const int64_t m = m0 + m_loc;
+        const bool in_m = in_m_[a];
         float v[4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int64_t n = n0 + n_loc + e;
+          const int64_t n = nb + e;
           const bool in_n = n < p.N;
-          const float bias_n = (p.bias && in_n) ? p.bias[n] : 0.f;
+          const float bias_n = bias4[e];
           if constexpr (INT8) {
             const int32_t raw = acc[a][b][4 * i4 + e];
             if (p.acc_out && in_m && in_n) p.acc_out[m * p.N + n] = raw;
             // y = fp32(acc) * (s_a * s_w) + b, each operation rounded separately (no FMA).
-            float y = static_cast<float>(raw) * (sa_m * (in_n ? p.s_w[n] : 0.f));
+            float y = static_cast<float>(raw) * (sa_m[a] * sw4[e]);
             if (p.bias) y = y + bias_n;
             v[e] = y;
+          } else if constexpr (LNF) {
+            v[e] = ln_fold(acc[a][b][4 * i4 + e], mean_m[a], rstd_m[a], cs4[e], bias_n);
           } else {
             v[e] = acc[a][b][4 * i4 + e] + bias_n;
           }
           if constexpr (GELU) v[e] = gelu_erf(to_f32(from_f32<TO>(v[e])));
-          if (!valid) v[e] = 0.f;
+          if (!valid_[a]) v[e] = 0.f;
         }
         if constexpr (STAGE_C) {
           typedef TO to4 __attribute__((ext_vector_type(4)));
@@ -446,7 +497,7 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
               if (n >= p.N) continue;
               float y = to_f32(from_f32<TO>(v[e]));  // the projection output, rounded once
               if (p.R) y = y + to_f32(static_cast<const TO*>(p.R)[m * p.ldr + n]);
-              if (!valid && (p.epi & EPI_ZERO_MASKED)) y = 0.f;
+              if (!valid_[a] && (p.epi & EPI_ZERO_MASKED)) y = 0.f;
               store_out<TO>(p.C, m * p.ldc + n, y);
             }
           }
@@ -540,7 +591,7 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
 // U chunk pairs per wave requested before the first MFMA. The NWS partial tiles are summed
 // through LDS in wave order (deterministic), then bias, row mask and residual are applied per
 // element as in gemm_kernel's epilogue and the tile is written row by row.
-template <int NWS, bool GELU>
+template <int NWS, bool GELU, bool LNF>
 __global__ __launch_bounds__(64 * NWS) void gemm_f32_splitk(GemmArgs p) {
   constexpr int U = 4;
   constexpr int PITCH = 65;  // padded: the reduction reads 32 features of one token per half-wave
@@ -589,7 +640,10 @@ __global__ __launch_bounds__(64 * NWS) void gemm_f32_splitk(GemmArgs p) {
     float v = red[0][i][l];
 #pragma unroll
     for (int w = 1; w < NWS; ++w) v += red[w][i][l];
-    if (p.bias) v = v + p.bias[n];
+    if constexpr (LNF)
+      v = ln_fold(v, p.ln_stats[2 * m], p.ln_stats[2 * m + 1], p.ln_colsum[n], p.bias ? p.bias[n] : 0.f);
+    else if (p.bias)
+      v = v + p.bias[n];
     if constexpr (GELU) v = gelu_erf(v);
     const bool masked = p.row_valid && p.row_valid[m] == 0;
     if (masked) v = 0.f;
@@ -606,10 +660,14 @@ int launch_gemm_f32_splitk(const GemmArgs& a, hipStream_t stream) {
   const dim3 grid(static_cast<unsigned>(tiles)), block(64 * NWS);
   // GELU is a compile-time variant: as a run-time option its inlined code in the unrolled
   // epilogue slowed every projection by ~10%
-  if (a.epi & EPI_GELU)
-    hipLaunchKernelGGL((gemm_f32_splitk<NWS, true>), grid, block, 0, stream, a);
-  else
-    hipLaunchKernelGGL((gemm_f32_splitk<NWS, false>), grid, block, 0, stream, a);
+  const bool lnf = a.ln_stats != nullptr;
+  if (a.epi & EPI_GELU) {
+    if (lnf) hipLaunchKernelGGL((gemm_f32_splitk<NWS, true, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((gemm_f32_splitk<NWS, true, false>), grid, block, 0, stream, a);
+  } else {
+    if (lnf) hipLaunchKernelGGL((gemm_f32_splitk<NWS, false, true>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((gemm_f32_splitk<NWS, false, false>), grid, block, 0, stream, a);
+  }
   return static_cast<int>(hipGetLastError());
 }
 
@@ -628,14 +686,34 @@ int launch_gemm(const GemmArgs& a, hipStream_t stream) {
   // GELU is a compile-time variant (as a run-time option its inlined code in the unrolled
   // epilogue slowed every projection by ~10%)
   const bool gelu = (a.epi & EPI_GELU) != 0;
+  if constexpr (!INT8) {
+    // the LayerNorm fold, likewise a compile-time variant (16-bit QKV / FFN-in outputs keep
+    // their input type or the fp16 attention core type; fp32 stays fp32)
+    constexpr bool LNF_OK = __is_same(T, TO) || __is_same(TO, _Float16);
+    if (a.ln_stats != nullptr) {
+      if constexpr (LNF_OK) {
+        if (direct && gelu)
+          hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, false, true, true, true>), grid, block, 0, stream, a);
+        else if (direct)
+          hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, false, true, false, true>), grid, block, 0, stream, a);
+        else if (gelu)
+          hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, false, false, true, true>), grid, block, 0, stream, a);
+        else
+          hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, false, false, false, true>), grid, block, 0, stream, a);
+        return static_cast<int>(hipGetLastError());
+      } else {
+        return MI355_E_UNSUPPORTED;
+      }
+    }
+  }
   if (direct && gelu)
-    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, true, true>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, true, true, false>), grid, block, 0, stream, a);
   else if (direct)
-    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, true, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, true, false, false>), grid, block, 0, stream, a);
   else if (gelu)
-    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, false, true>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, false, true, false>), grid, block, 0, stream, a);
   else
-    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, false, false>), grid, block, 0, stream, a);
+    hipLaunchKernelGGL((gemm_kernel<T, TO, BM, BN, WM, WN, INT8, false, false, false>), grid, block, 0, stream, a);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -667,7 +745,8 @@ int launch_by_out(const GemmArgs& a, hipStream_t s) {
 namespace {
 int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, const void* W, int64_t ldw,
                    const float* bias, const void* R, int64_t ldr, void* C, int64_t ldc, int64_t M,
-                   int64_t N, int64_t K, const uint8_t* row_valid, void* stream, int epi = 0) {
+                   int64_t N, int64_t K, const uint8_t* row_valid, void* stream, int epi = 0,
+                   const float* ln_stats = nullptr, const float* ln_colsum = nullptr) {
   if (M < 0 || N < 0 || K < 0) return MI355_E_BAD_SIZE;
   if (M == 0 || N == 0) return MI355_OK;
   if (!A || !W || !C) return MI355_E_NULL_POINTER;
@@ -695,6 +774,8 @@ int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, cons
   a.K = K;
   a.out_dtype = out_dtype;
   a.epi = epi;
+  a.ln_stats = ln_stats;
+  a.ln_colsum = ln_colsum;
   hipStream_t s = static_cast<hipStream_t>(stream);
   switch (in_dtype) {
     case MI355_F16: return launch_by_out<_Float16, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
@@ -745,6 +826,50 @@ extern "C" int mi355_gemm_bias_residual_zero_masked(int in_dtype, int out_dtype,
   if (M > 0 && N > 0 && !R) return MI355_E_NULL_POINTER;
   return gemm_bias_impl(in_dtype, out_dtype, A, lda, W, ldw, bias, R, ldr, C, ldc, M, N, K,
                         row_valid, stream, EPI_ZERO_MASKED);
+}
+
+namespace {
+// Checks shared by the LayerNorm-folded entry points; 0 when the arguments are acceptable.
+int ln_gemm_check(int in_dtype, int out_dtype, const void* X, int64_t ldx, const void* W,
+                  const float* colsum, float eps, void* C, int64_t M, int64_t N, int64_t K, int epi) {
+  if (M < 0 || N < 0 || K <= 0) return MI355_E_BAD_SIZE;
+  if (M == 0 || N == 0) return MI355_OK;
+  if (!X || !W || !C || !colsum) return MI355_E_NULL_POINTER;
+  if (in_dtype != MI355_F32 && in_dtype != MI355_F16 && in_dtype != MI355_BF16) return MI355_E_BAD_DTYPE;
+  if (out_dtype != MI355_F32 && out_dtype != MI355_F16 && out_dtype != MI355_BF16) return MI355_E_BAD_DTYPE;
+  // 16-bit outputs: the input type, or fp16 (the attention core type of a bf16 model)
+  if (in_dtype != out_dtype && out_dtype != MI355_F16) return MI355_E_UNSUPPORTED;
+  if (epi & ~MI355_EPI_GELU) return MI355_E_UNSUPPORTED;
+  if (!(eps >= 0.f)) return MI355_E_BAD_SIZE;
+  const int64_t epv = in_dtype == MI355_F32 ? 4 : 8;
+  if (K % epv || ldx % epv || !aligned16(X)) return MI355_E_ALIGNMENT;
+  if (ldx < K) return MI355_E_BAD_SIZE;
+  if (K / epv > 64 * 16) return MI355_E_UNSUPPORTED;  // the statistics pass holds a row per wave
+  return MI355_OK;
+}
+
+int ln_gemm_run(int in_dtype, int out_dtype, const void* X, int64_t ldx, const void* W, int64_t ldw,
+                const float* colsum, const float* bias, float eps, float* stats, void* C,
+                int64_t ldc, int64_t M, int64_t N, int64_t K, int epi, void* stream) {
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  int rc = mi355_internal_ln_stats(in_dtype, X, ldx, eps, stats, M, K, s);
+  if (rc != MI355_OK) return rc;
+  return gemm_bias_impl(in_dtype, out_dtype, X, ldx, W, ldw, bias, nullptr, 0, C, ldc, M, N, K,
+                        nullptr, stream, (epi & MI355_EPI_GELU) ? EPI_GELU : 0, stats, colsum);
+}
+}  // namespace
+
+extern "C" int mi355_layernorm_gemm_bias(int in_dtype, int out_dtype, const void* X, int64_t ldx,
+                                         const void* W, int64_t ldw, const float* colsum,
+                                         const float* bias, float eps, float* stats, void* C,
+                                         int64_t ldc, int64_t M, int64_t N, int64_t K, int epi,
+                                         void* stream) {
+  int rc = ln_gemm_check(in_dtype, out_dtype, X, ldx, W, colsum, eps, C, M, N, K, epi);
+  if (rc != MI355_OK || M == 0 || N == 0) return rc;
+  if (!stats) return MI355_E_NULL_POINTER;
+  if (reinterpret_cast<uintptr_t>(stats) & 7u) return MI355_E_ALIGNMENT;
+  return ln_gemm_run(in_dtype, out_dtype, X, ldx, W, ldw, colsum, bias, eps, stats, C, ldc, M, N,
+                     K, epi, stream);
 }
 
 extern "C" int mi355_gemm_i8(const int8_t* A, const int8_t* W, const float* s_a, const float* s_w,

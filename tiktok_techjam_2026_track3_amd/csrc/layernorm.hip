@@ -81,6 +81,77 @@ __global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, i
   }
 }
 
+// Row statistics only: stats[2 row] = mean, stats[2 row + 1] = rstd, computed exactly as in
+// layernorm_rows (the same loads, sums and rounding), for GEMMs that fold the normalisation into
+// their epilogue (mi355_layernorm_gemm_bias). Reads the row once, writes 8 bytes. A row whose
+// variance is exactly 0 (every element equals the mean, so its normalised values are exactly
+// beta) gets rstd 0: the folded epilogue then yields the bias term alone instead of
+// 1/sqrt(eps) times the fp32 rounding residue of x W'^T - mean colsum.
+template <typename T, int NV>
+__global__ __launch_bounds__(256) void layernorm_stats(const T* __restrict__ X, int64_t ldx, float eps,
+                                                       float* __restrict__ stats, int64_t M, int K) {
+  constexpr int EPV = 16 / static_cast<int>(sizeof(T));
+  typedef T tv __attribute__((ext_vector_type(EPV)));
+  const int lane = threadIdx.x & 63;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  if (row >= M) return;
+  const int nvec = K / EPV;
+  const T* xr = X + row * ldx;
+  float xs[NV][EPV];
+  float sum = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    const int vi = lane + 64 * j;
+    tv v = {};
+    if (vi < nvec) v = *reinterpret_cast<const tv*>(xr + static_cast<int64_t>(vi) * EPV);
+#pragma unroll
+    for (int e = 0; e < EPV; ++e) {
+      xs[j][e] = to_f32(v[e]);
+      sum += xs[j][e];
+    }
+  }
+  const float mean = wave_sum(sum) / static_cast<float>(K);
+  float sq = 0.f;
+#pragma unroll
+  for (int j = 0; j < NV; ++j) {
+    if (lane + 64 * j < nvec) {
+#pragma unroll
+      for (int e = 0; e < EPV; ++e) {
+        const float d = xs[j][e] - mean;
+        sq += d * d;
+      }
+    }
+  }
+  const float var = wave_sum(sq) / static_cast<float>(K);
+  if (lane == 0) {
+    typedef float f32x2 __attribute__((ext_vector_type(2)));
+    *reinterpret_cast<f32x2*>(stats + 2 * row) = f32x2{mean, var > 0.f ? 1.0f / sqrtf(var + eps) : 0.f};
+  }
+}
+
+template <typename T>
+int launch_stats(const void* X, int64_t ldx, float eps, float* stats, int64_t M, int64_t K,
+                 hipStream_t s) {
+  constexpr int EPV = 16 / static_cast<int>(sizeof(T));
+  const int64_t nvec = K / EPV;
+  const int64_t blocks = (M + 3) / 4;
+  if (blocks > 0x7fffffffLL) return MI355_E_BAD_SIZE;
+  const dim3 grid(static_cast<unsigned>(blocks)), block(256);
+  const T* x = static_cast<const T*>(X);
+  const int k = static_cast<int>(K);
+  if (nvec <= 64)
+    hipLaunchKernelGGL((layernorm_stats<T, 1>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+  else if (nvec <= 128)
+    hipLaunchKernelGGL((layernorm_stats<T, 2>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+  else if (nvec <= 256)
+    hipLaunchKernelGGL((layernorm_stats<T, 4>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+  else if (nvec <= 512)
+    hipLaunchKernelGGL((layernorm_stats<T, 8>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+  else
+    hipLaunchKernelGGL((layernorm_stats<T, 16>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+  return static_cast<int>(hipGetLastError());
+}
+
 template <typename T>
 int launch_ln(const void* X, int64_t ldx, const void* gamma, const void* beta, float eps, void* Y,
               int64_t ldy, int64_t M, int64_t K, const uint8_t* rv, hipStream_t s) {
@@ -108,6 +179,17 @@ int launch_ln(const void* X, int64_t ldx, const void* gamma, const void* beta, f
 }
 
 }  // namespace
+
+// Library-internal (declared in common.h): the statistics pass of mi355_layernorm_gemm_bias.
+// Arguments are validated by the caller.
+int mi355_internal_ln_stats(int dtype, const void* X, int64_t ldx, float eps, float* stats,
+                            int64_t M, int64_t K, hipStream_t s) {
+  switch (dtype) {
+    case MI355_F16: return launch_stats<_Float16>(X, ldx, eps, stats, M, K, s);
+    case MI355_BF16: return launch_stats<__bf16>(X, ldx, eps, stats, M, K, s);
+    default: return launch_stats<float>(X, ldx, eps, stats, M, K, s);
+  }
+}
 
 extern "C" int mi355_layernorm_masked(int dtype, const void* X, int64_t ldx, const void* gamma,
                                       const void* beta, float eps, void* Y, int64_t ldy, int64_t M,

@@ -14,9 +14,10 @@ nothing synchronises the host, and every buffer is allocated through torch's cac
 the static buffers, replays, and returns a fresh copy of the output (callers own their output,
 as with the eager forward). A captured graph is tied to the shapes, dtype, device, causal flag
 and mask presence it was recorded with, and to the module's parameters at capture time (the
-graph reads the packed weights the module had then, and keeps them alive): calling it with
-other inputs, after the parameters changed, or after the module rebuilt or dropped its packed
-weights (``.to()``, ``load_state_dict``), raises.
+graph reads the packed weights -- and, for the attention half, the LayerNorm-folded QKV weights --
+the module had then, and keeps them alive): calling it with other inputs, after the parameters
+(the module's or the norm's) changed, or after the module rebuilt or dropped its derived weights
+(``.to()``, ``load_state_dict``), raises.
 """
 from __future__ import annotations
 
@@ -56,9 +57,12 @@ class GraphedForward:
         # cache (_apply, load_state_dict), and __call__ refuses to replay once the module's
         # cache entry is no longer the one captured.
         self._cache = self.module.__dict__.get("_mi355_pack")
+        # likewise the LayerNorm-folded QKV weights that forward_residual reads
+        self._ln_cache = self.module.__dict__.get("_mi355_lnpack")
 
     def _cache_current(self) -> bool:
-        return self.module.__dict__.get("_mi355_pack") is self._cache
+        return (self.module.__dict__.get("_mi355_pack") is self._cache
+                and self.module.__dict__.get("_mi355_lnpack") is getattr(self, "_ln_cache", None))
 
     def _params_stamp(self):
         mods = [self.module] + ([self.norm] if self.norm is not None else [])

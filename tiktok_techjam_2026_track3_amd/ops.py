@@ -142,6 +142,68 @@ def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[t
     return out
 
 
+def fold_layernorm(weight: torch.Tensor, bias: Optional[torch.Tensor],
+                   gamma: Optional[torch.Tensor], beta: Optional[torch.Tensor],
+                   dtype: torch.dtype) -> Tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Host-side fold of a LayerNorm (gamma, beta) into the projection that consumes it, for
+    ``layernorm_linear``: returns ``(Wf [N, K] of dtype, colsum [N] fp32, bias' [N] fp32)`` with
+    ``Wf = dtype(W * gamma)``, ``colsum = sum_k Wf[:, k]`` (of the rounded Wf, so the epilogue's
+    mean subtraction cancels exactly against the weights the GEMM uses) and
+    ``bias' = b + W @ beta``; the sums are formed in fp64. Run once per weight version."""
+    with torch.no_grad():
+        w64 = weight.detach().to(torch.float64)
+        g = gamma.detach().to(torch.float64) if gamma is not None else None
+        wf = (w64 * g[None, :] if g is not None else w64).to(dtype).contiguous()
+        colsum = wf.to(torch.float64).sum(dim=1).to(torch.float32).contiguous()
+        b = (bias.detach().to(torch.float64) if bias is not None
+             else torch.zeros(weight.shape[0], dtype=torch.float64, device=weight.device))
+        if beta is not None:
+            b = b + w64 @ beta.detach().to(torch.float64)
+        return wf, colsum, b.to(torch.float32).contiguous()
+
+
+def layernorm_linear(x: torch.Tensor, weight: torch.Tensor, colsum: torch.Tensor,
+                     bias: Optional[torch.Tensor], eps: float = 1e-5,
+                     out_dtype: Optional[torch.dtype] = None, gelu: bool = False,
+                     out: Optional[torch.Tensor] = None,
+                     stats: Optional[torch.Tensor] = None) -> torch.Tensor:
+    """``nn.Linear(nn.LayerNorm(x))`` (optionally followed by the exact GELU) without writing the
+    normalised rows: ``weight``, ``colsum`` and ``bias`` come from ``fold_layernorm``. ``x`` is a
+    2-D row-strided tensor (unit column stride); the row statistics go to ``stats`` ([M, 2] fp32
+    workspace, allocated when not given). ``out_dtype`` defaults to x's dtype (a bf16 input may
+    give fp16)."""
+    _on_gpu(x, weight, colsum, bias, out, stats)
+    if x.dim() != 2 or weight.dim() != 2 or x.stride(1) != 1:
+        raise ValueError("layernorm_linear expects a 2-D x with unit column stride and 2-D weight")
+    M, K = x.shape
+    N, K2 = weight.shape
+    if K2 != K:
+        raise ValueError(f"inner sizes differ: x has K={K}, weight has K={K2}")
+    if weight.dtype != x.dtype or not weight.is_contiguous():
+        raise ValueError("weight must be contiguous and of x's dtype")
+    if colsum.shape != (N,) or colsum.dtype != torch.float32 or not colsum.is_contiguous():
+        raise ValueError(f"colsum must be a contiguous fp32 tensor of shape ({N},)")
+    if bias is not None and (bias.shape != (N,) or bias.dtype != torch.float32
+                             or not bias.is_contiguous()):
+        raise ValueError(f"bias must be a contiguous fp32 tensor of shape ({N},)")
+    odt = out_dtype or (out.dtype if out is not None else x.dtype)
+    if out is None:
+        out = torch.empty((M, N), device=x.device, dtype=odt)
+    elif out.shape != (M, N) or out.dtype != odt or out.stride(1) != 1:
+        raise ValueError("out must be [M, N] of out_dtype with unit column stride")
+    if stats is None:
+        stats = torch.empty((M, 2), device=x.device, dtype=torch.float32)
+    elif stats.shape != (M, 2) or stats.dtype != torch.float32 or not stats.is_contiguous():
+        raise ValueError(f"stats must be a contiguous fp32 tensor of shape ({M}, 2)")
+    st = _lib.lib().mi355_layernorm_gemm_bias(
+        _lib.dtype_code(x.dtype), _lib.dtype_code(odt), x.data_ptr(), x.stride(0),
+        weight.data_ptr(), weight.stride(0), colsum.data_ptr(),
+        bias.data_ptr() if bias is not None else 0, float(eps), stats.data_ptr(), out.data_ptr(),
+        out.stride(0), M, N, K, _lib.EPI_GELU if gelu else 0, _stream(x))
+    _lib.check("mi355_layernorm_gemm_bias", st)
+    return out
+
+
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[torch.Tensor] = None,
               scale: Optional[float] = None, causal: bool = False,
               key_valid: Optional[torch.Tensor] = None) -> torch.Tensor:

@@ -5,13 +5,17 @@ and ``Transformer`` mirrors ``BaselineTransformer`` / ``UserOptimizedTransformer
 same constructor arguments, attribute and parameter names (so a baseline state dict loads with
 ``strict=True``) and forward signatures. A block forward is seven launches on the current stream:
 
-  1. LayerNorm kernel                     h = norm1(x)                         (:139)
-  2. packed QKV projection                qkv = h W_qkv^T + b_qkv               (:93-95)
-  3. streamed attention                   ctx                                  (:97-117)
-  4. out projection + residual epilogue   x1 = x + out_proj(ctx), masked rows x (:118-121, :139)
-  5. LayerNorm kernel                     h2 = norm2(x1)                       (:141)
-  6. ffn_in + GELU epilogue               g = gelu(ffn_in(h2))                 (:141)
-  7. ffn_out + residual + row-mask epilogue  y = x1 + ffn_out(g), masked rows 0  (:141-144)
+  1. norm1 statistics + packed QKV projection with norm1 folded in
+                                          qkv = norm1(x) W_qkv^T + b_qkv        (:139, :93-95)
+  2. streamed attention                   ctx                                  (:97-117)
+  3. out projection + residual epilogue   x1 = x + out_proj(ctx), masked rows x (:118-121, :139)
+  4. norm2 statistics + ffn_in with norm2 folded in and the GELU epilogue
+                                          g = gelu(ffn_in(norm2(x1)))          (:141)
+  5. ffn_out + residual + row-mask epilogue  y = x1 + ffn_out(g), masked rows 0  (:141-144)
+
+(1 and 4 are two launches each: a row-statistics pass and the projection, whose epilogue applies
+the mean, rstd and beta; gamma is folded into the weights. bf16 models, and
+``SelfAttention.fold_norm = False``, run the LayerNorms as their own row kernels instead.)
 
 and the model adds one masked LayerNorm launch for ``final_norm`` + masked_fill (:168-171).
 Every rounding point of the reference's dtype arithmetic is kept: each nn.Linear output is
@@ -60,6 +64,23 @@ def _ffn_weights(block: nn.Module, dtype: torch.dtype, device: torch.device):
     return value
 
 
+def _ffn_in_folded(block: nn.Module, dtype: torch.dtype, device: torch.device):
+    """(Wf [ffn, d] in dtype, colsum fp32, bias' fp32): norm2 folded into ffn_in
+    (ops.fold_layernorm), cached on the block like ``_ffn_weights``."""
+    n2 = block.norm2
+    key = ("ffn_in_ln", dtype, device, _stamp(block.ffn_in.weight, block.ffn_in.bias, n2.weight,
+                                              n2.bias), float(n2.eps))
+    entry = block.__dict__.get("_mi355_ffn_ln")
+    if entry is not None and entry[0] == key:
+        return entry[1]
+    with torch.no_grad():
+        w = block.ffn_in.weight.to(device=device)
+        b = None if block.ffn_in.bias is None else block.ffn_in.bias.to(device=device)
+        value = ops.fold_layernorm(w, b, n2.weight, n2.bias, dtype)
+    block.__dict__["_mi355_ffn_ln"] = (key, value)
+    return value
+
+
 def _ffn_weights_i8(block: nn.Module, device: torch.device):
     """(W_in int8 [ffn, d], s_in, b_in, W_out int8 [d, ffn], s_out, b_out): the weight recipe of
     ``_int8_pack`` (k008_int8_gemm.py:154-158) applied by the quantisation kernel to the fp32
@@ -101,9 +122,12 @@ def block_forward(block: nn.Module, x: torch.Tensor, valid_token_mask: Optional[
     kernels, for any module with the block's attributes whose ``attention`` is a SelfAttention
     (or an Int8SelfAttention: the W8A8 block).
 
-    ``marks(stage)`` is called before each launch ("norm", "qkv", "attn", "out", "norm2",
-    "ffn_in", "ffn_out"; the int8 block adds its quantisation launches) and after the last
-    ("end"). ``keep`` (a dict) receives the int8 block's intermediates."""
+    With ``attention.folds_norm(dtype)`` (fp32 / fp16 by default) norm1 is folded into the QKV projection and norm2
+    into ffn_in (row-statistics pass + projection epilogue, ``ops.layernorm_linear``), so neither
+    normalised activation is written. ``marks(stage)`` is called before each launch ("qkv",
+    "attn", "out", "ffn_in", "ffn_out"; unfolded, "norm" and "norm2" before the LayerNorm
+    kernels; the int8 block adds its quantisation launches) and after the last ("end").
+    ``keep`` (a dict) receives the int8 block's intermediates."""
     mark = marks or (lambda _stage: None)
     attn = block.attention
     if not isinstance(attn, SelfAttention):
@@ -122,10 +146,15 @@ def block_forward(block: nn.Module, x: torch.Tensor, valid_token_mask: Optional[
     x1 = x1.reshape(B * S, d)
     w2, b2 = _norm_params(block.norm2, x)
     w_in, b_in, w_out, b_out = _ffn_weights(block, x.dtype, x.device)
-    mark("norm2")
-    h2 = ops.layer_norm(x1, w2, b2, block.norm2.eps)
-    mark("ffn_in")
-    g = ops.linear(h2, w_in, b_in, gelu=True, out_dtype=x.dtype)
+    if attn.folds_norm(x.dtype):
+        wf, colsum, bf = _ffn_in_folded(block, x.dtype, x.device)
+        mark("ffn_in")
+        g = ops.layernorm_linear(x1, wf, colsum, bf, block.norm2.eps, gelu=True)
+    else:
+        mark("norm2")
+        h2 = ops.layer_norm(x1, w2, b2, block.norm2.eps)
+        mark("ffn_in")
+        g = ops.linear(h2, w_in, b_in, gelu=True, out_dtype=x.dtype)
     mark("ffn_out")
     y = ops.linear(g, w_out, b_out, residual=x1, row_valid=row_valid, zero_masked_rows=True,
                    out_dtype=x.dtype)
