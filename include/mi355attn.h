@@ -221,6 +221,25 @@ int mi355_layernorm_gemm_bias(int in_dtype, int out_dtype, const void* X, int64_
                               float eps, float* stats, void* C, int64_t ldc, int64_t M, int64_t N,
                               int64_t K, int epi, void* stream);
 
+/* largest M of mi355_layernorm_gemm_bias_noalloc (its statistics array: 8 MiB per GPU) */
+#define MI355_NOALLOC_MAX_ROWS (1 << 20)
+
+/*
+ * mi355_layernorm_gemm_bias without the `stats` workspace: the row statistics go to a file-scope
+ * device array of the library (MI355_NOALLOC_MAX_ROWS rows, 8 MiB per GPU, held until the process
+ * ends), so the call allocates nothing and takes no workspace. No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid allocation). M > MI355_NOALLOC_MAX_ROWS returns
+ * MI355_E_BAD_SIZE. All calls on one GPU share that array: calls that overlap on one GPU (on
+ * different streams, or from several threads) race and must be ordered by the caller. The first
+ * call on a device looks the array's address up (hipGetSymbolAddress) and keeps it. Otherwise as
+ * mi355_layernorm_gemm_bias, with the same kernels and results.
+ */
+int mi355_layernorm_gemm_bias_noalloc(int in_dtype, int out_dtype, const void* X, int64_t ldx,
+                                      const void* W, int64_t ldw, const float* colsum,
+                                      const float* bias, float eps, void* C, int64_t ldc, int64_t M,
+                                      int64_t N, int64_t K, int epi, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -59,6 +59,11 @@ _SIGNATURES = {
         [C.c_int, C.c_int, _P, _I64, _P, _I64, _P, _P, C.c_float, _P, _P, _I64, _I64, _I64, _I64,
          C.c_int, _P],
     ),
+    "mi355_layernorm_gemm_bias_noalloc": (
+        C.c_int,
+        [C.c_int, C.c_int, _P, _I64, _P, _I64, _P, _P, C.c_float, _P, _I64, _I64, _I64, _I64,
+         C.c_int, _P],
+    ),
     "mi355_gemm_i8_epilogue": (
         C.c_int,
         [_P, _P, _P, _P, _P, C.c_int, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, C.c_int, _P],

@@ -9,6 +9,8 @@
 // epilogue stages the finished tile in LDS and writes it back in 16-byte row chunks.
 #include "common.h"
 
+#include <mutex>
+
 // interleave the LDS fragment reads of k-slice j+1 with the MFMAs of slice j: 1 = scheduler
 // hints, 2 = explicit issue order (MFMA, read, MFMA, read, ... fenced by sched_barrier);
 // measured on the projection shapes: 2 is 3-5% faster than 1
@@ -868,6 +870,65 @@ extern "C" int mi355_layernorm_gemm_bias(int in_dtype, int out_dtype, const void
   if (rc != MI355_OK || M == 0 || N == 0) return rc;
   if (!stats) return MI355_E_NULL_POINTER;
   if (reinterpret_cast<uintptr_t>(stats) & 7u) return MI355_E_ALIGNMENT;
+  return ln_gemm_run(in_dtype, out_dtype, X, ldx, W, ldw, colsum, bias, eps, stats, C, ldc, M, N,
+                     K, epi, stream);
+}
+
+// ---- the allocation-free variant: row statistics in a file-scope device array
+// Each GPU the library runs on holds its own copy of `scratch` (MI355_NOALLOC_MAX_ROWS rows of
+// (mean, rstd): 8 MiB) until the process ends. Host code never passes the array's name to a
+// kernel (on the host it is only a stand-in for the symbol): it uses the device address that
+// hipGetSymbolAddress returns for the current device, looked up once per device.
+static __device__ __align__(256) float scratch[2 * MI355_NOALLOC_MAX_ROWS];
+
+namespace {
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_mu;
+float* g_scratch_ptr[kMaxDevices] = {};
+
+// device address of `scratch` on the device that owns `stream` (the current device for the
+// null stream); nullptr after a HIP error, whose code goes to *rc
+float* scratch_for(hipStream_t stream, int* rc) {
+  int cur = 0;
+  hipError_t e = hipGetDevice(&cur);
+  if (e != hipSuccess) { *rc = static_cast<int>(e); return nullptr; }
+  int dev = cur;
+  if (stream != nullptr) {
+    e = hipStreamGetDevice(stream, &dev);
+    if (e != hipSuccess) { *rc = static_cast<int>(e); return nullptr; }
+  }
+  if (dev < 0 || dev >= kMaxDevices) { *rc = MI355_E_UNSUPPORTED; return nullptr; }
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    if (dev != cur && (e = hipSetDevice(dev)) != hipSuccess) { *rc = static_cast<int>(e); return nullptr; }
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (dev != cur) {
+      const hipError_t e2 = hipSetDevice(cur);
+      if (e == hipSuccess) e = e2;
+    }
+    if (e != hipSuccess || ptr == nullptr) {
+      *rc = e != hipSuccess ? static_cast<int>(e) : MI355_E_NULL_POINTER;
+      return nullptr;
+    }
+    g_scratch_ptr[dev] = static_cast<float*>(ptr);
+  }
+  return g_scratch_ptr[dev];
+}
+}  // namespace
+
+extern "C" int mi355_layernorm_gemm_bias_noalloc(int in_dtype, int out_dtype, const void* X,
+                                                 int64_t ldx, const void* W, int64_t ldw,
+                                                 const float* colsum, const float* bias, float eps,
+                                                 void* C, int64_t ldc, int64_t M, int64_t N,
+                                                 int64_t K, int epi, void* stream) {
+  int rc = ln_gemm_check(in_dtype, out_dtype, X, ldx, W, colsum, eps, C, M, N, K, epi);
+  if (rc != MI355_OK || M == 0 || N == 0) return rc;
+  if (M > MI355_NOALLOC_MAX_ROWS) return MI355_E_BAD_SIZE;
+  float* stats = scratch_for(static_cast<hipStream_t>(stream), &rc);
+  if (stats == nullptr) return rc;
+  // every row's statistics are written by the statistics pass before the projection reads
+  // them, so nothing left by an earlier call needs clearing
   return ln_gemm_run(in_dtype, out_dtype, X, ldx, W, ldw, colsum, bias, eps, stats, C, ldc, M, N,
                      K, epi, stream);
 }
