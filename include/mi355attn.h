@@ -49,8 +49,10 @@ const char* mi355_status_string(int status);
  * Dense projection  C[M,N] = A[M,K] · W[N,K]^T + bias[N]   (nn.Linear semantics).
  * Replaces q_proj/k_proj/v_proj/out_proj (torch_transformer_benchmark.py:93-95, :118) and the
  * packed-QKV F.linear of the optimised route (Project/submission/dispatcher_region.py:789-792,
- * :1025, :1085). A and W share in_dtype (F32, F16, BF16); C has out_dtype (F16 or BF16 for
- * 16-bit inputs, which may differ from in_dtype; F32 for F32 inputs). bias is fp32 or NULL.
+ * :1025, :1085). A and W share in_dtype (F32, F16, BF16); C has out_dtype: any of the three for
+ * 16-bit inputs, F32 or F16 for F32 inputs (F16 carries an fp32 model's q/k/v into the fp16
+ * attention core; F32 out of a 16-bit product returns its context projection to fp32). bias
+ * is fp32 or NULL.
  * Accumulation and the bias add are fp32; C is rounded once (round-to-nearest-even).
  * Rows m with row_valid[m] == 0 are written as exact zeros (the output-row mask of
  * torch_transformer_benchmark.py:120-121); row_valid may be NULL (all rows valid).

@@ -68,7 +68,8 @@ def test_gemm_argument_validation():
     assert h.mi355_gemm_bias(7, 1, fake, 64, fake, 64, None, fake, 64, 4, 64, 64, None, None) == codes["MI355_E_BAD_DTYPE"]
     assert h.mi355_gemm_bias(1, 1, fake, 64, fake, 64, None, fake, 64, 4, 64, 60, None, None) == codes["MI355_E_ALIGNMENT"]
     assert h.mi355_gemm_bias(1, 1, fake + 2, 64, fake, 64, None, fake, 64, 4, 64, 64, None, None) == codes["MI355_E_ALIGNMENT"]
-    assert h.mi355_gemm_bias(0, 1, fake, 64, fake, 64, None, fake, 64, 4, 64, 64, None, None) == codes["MI355_E_UNSUPPORTED"]
+    # fp32 inputs give fp32 or fp16 (an fp32 model's fp16 attention core), never bf16
+    assert h.mi355_gemm_bias(0, 2, fake, 64, fake, 64, None, fake, 64, 4, 64, 64, None, None) == codes["MI355_E_UNSUPPORTED"]
     assert h.mi355_gemm_bias(1, 1, fake, 32, fake, 64, None, fake, 64, 4, 64, 64, None, None) == codes["MI355_E_BAD_SIZE"]
     # empty problems are a successful no-op
     assert h.mi355_gemm_bias(1, 1, None, 64, None, 64, None, None, 64, 0, 64, 64, None, None) == 0

@@ -48,9 +48,15 @@ GEMM_SHAPES = [(1, 64, 64), (128, 768, 256), (300, 200, 136), (513, 130, 1024), 
                                              (torch.bfloat16, torch.bfloat16),
                                              (torch.float32, torch.float32),
                                              (torch.bfloat16, torch.float16),
-                                             (torch.float16, torch.bfloat16)])
+                                             (torch.float16, torch.bfloat16),
+                                             (torch.float32, torch.float16),
+                                             (torch.float16, torch.float32),
+                                             (torch.bfloat16, torch.float32)])
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
 def test_linear_error_bound(gpu, dtype, out_dtype, M, N, K):
+    """Every operand / output type pair, on shapes that take the split-K kernel (at most 512
+    tiles of 32 x 32: the first four), the 256 x 256 (16-bit) or 128 x 128 / 64 x 64 (fp32)
+    tiled kernel, the LDS-DMA loader (K a multiple of the K step) and the register-staged one."""
     ops = _ops()
     a = _rand((M, K), dtype, 1)
     w = _rand((N, K), dtype, 2, scale=K ** -0.5)
@@ -124,7 +130,7 @@ def _attn_check(gpu, dtype, B, H, Sq, Sk, hd, causal, key_valid=None, packed=Fal
     qk_abs = (tq.abs() @ tk.abs().transpose(-2, -1)).amax(dim=-1, keepdim=True).transpose(1, 2)
     uq = UNIT[dtype] if dtype != torch.float32 else 0.0
     rel = 2 * up + 2.0 ** -18 + 2.0 ** -22 * logit2 + 2 * math.log(2) * uq * c * qk_abs
-    if dtype == torch.float16 and hd == 64:
+    if dtype == torch.float16 and hd in (32, 64):
         # the MFMA kernel sums a sub-tile's 32 rounded fp16 probabilities per lane in a 4-level
         # tree of packed fp16 adds: the row sum, and so the whole output row, carries up to 4
         # more fp16 roundings of relative error

@@ -16,12 +16,16 @@ A GPU forward is three launches on the current stream:
 per-token int8 activations, per-output-channel int8 weights, exact int32 accumulation, fp32
 dequantisation, fp16 SDPA.
 
-Precision policy: fp32 inputs run fp32 end to end; fp16 inputs run fp16 storage with fp32
-accumulation; bf16 inputs run the QKV projection on bf16 operands but store q/k/v, the
-probabilities and the context in fp16 (``bf16_core_dtype``), whose 3 extra mantissa bits keep
-the block within the elementwise 2e-3 / 2e-2 tolerance of fp32 math that a bf16-stored core
-misses; the output is bf16. Values beyond the fp16 range (65504) in q/k/v or the context become
-inf and surface as non-finite outputs; set ``bf16_core_dtype = torch.bfloat16`` for such models.
+Precision policy: fp16 inputs run fp16 storage with fp32 accumulation; bf16 inputs run the
+QKV projection on bf16 operands but store q/k/v, the probabilities and the context in fp16
+(``bf16_core_dtype``), whose 3 extra mantissa bits keep the block within the elementwise
+2e-3 / 2e-2 tolerance of fp32 math that a bf16-stored core misses; the output is bf16. fp32
+inputs run the QKV projection in fp32 and, at head dims 32 / 64 / 128, store q/k/v, the
+probabilities and the context in fp16 (``fp32_core_dtype``: the fp16 tiles of the reference's
+fp32 fast route) so attention runs on the matrix cores; the out projection reads that context
+and returns fp32. Other fp32 head dims, and ``fp32_core_dtype = torch.float32``, keep fp32 end
+to end. Values beyond the fp16 range (65504) in q/k/v or the context become inf and surface as
+non-finite outputs; set the core dtype attributes to the input dtype for such models.
 
 There is no CPU or eager-torch fallback: CPU inputs raise, and a missing library raises.
 Derived caches (packed / quantised weights) live in the instance ``__dict__`` and are dropped
@@ -39,6 +43,9 @@ from . import ops
 
 _CACHE_KEYS = ("_mi355_pack", "_mi355_lnpack")
 
+# head dims of the fp16 / bf16 matrix-core attention kernel (the others run on vector ALUs)
+MFMA_HEAD_DIMS = (32, 64, 128)
+
 
 def norm_stamp(norm: nn.Module) -> Tuple:
     """Identity of a LayerNorm's parameters (storage, version, dtype, device) and eps."""
@@ -50,6 +57,13 @@ class SelfAttention(nn.Module):
     """Multi-head self-attention with the reference's module API, on gfx950 kernels."""
 
     bf16_core_dtype = torch.float16
+    # fp32 models at the matrix-core head dims (32, 64, 128) keep the projections' operands in
+    # fp32 but carry q/k/v, the probabilities and the context in fp16, so attention runs on the
+    # fp16 MFMA kernel -- the fp16 tiles the reference's fast route uses for fp32 models
+    # (Project/submission/dispatcher_region.py:1017-1091); the out projection reads the fp16
+    # context with an fp16 copy of its weight and returns fp32. torch.float32 keeps the core
+    # in fp32 (the vector-ALU kernel).
+    fp32_core_dtype = torch.float16
     # forward_residual folds the LayerNorm into the QKV projection (row statistics pass + the
     # projection's epilogue) for fp32 and fp16 inputs; False runs the LayerNorm kernel and a
     # plain projection instead
@@ -107,7 +121,11 @@ class SelfAttention(nn.Module):
 
     def core_dtype(self, dtype: torch.dtype) -> torch.dtype:
         """Storage dtype of q/k/v, probabilities and context for input dtype ``dtype``."""
-        return self.bf16_core_dtype if dtype == torch.bfloat16 else dtype
+        if dtype == torch.bfloat16:
+            return self.bf16_core_dtype
+        if dtype == torch.float32 and self.head_dim in MFMA_HEAD_DIMS:
+            return self.fp32_core_dtype
+        return dtype
 
     def _packed_weights(self, dtype: torch.dtype, device: torch.device):
         """(W_qkv [3d, d] in the input dtype, b_qkv fp32, W_o [d, d] in the core dtype, b_o fp32)."""

@@ -12,7 +12,7 @@
 //   * probabilities are exp2(s*scale*log2e - m*scale*log2e) in fp32, rounded to the input dtype
 //     (the rounding point of torch_transformer_benchmark.py:111) and fed straight from registers
 //     as the B operand of O^T += V^T · P^T; each V^T fragment is built from the key-major V tile
-//     by two ds_read_b64_tr_b16 transpose reads; at head_dim 64 the fp16 row sums add the
+//     by two ds_read_b64_tr_b16 transpose reads; at head_dim 32 / 64 the fp16 row sums add the
 //     rounded probabilities of a sub-tile with packed fp16 adds and carry the total in fp32;
 //   * scores live in the log2 domain (Q pre-multiplied by scale*log2e) and every score MFMA chain
 //     starts from -mu, so exp2 consumes the MFMA output directly;
@@ -93,11 +93,15 @@ template <int NCH>
 MI355_DEVINL int swz(int r) {
   if constexpr (NCH >= 16)
     return ((r & 1) << 2) ^ (((r >> 1) & 1) * 10) ^ ((r >> 2) & 3);
-  else
+  else if constexpr (NCH == 8)
     return ((r & 1) << 1) ^ ((r & 2) << 1) ^ ((r >> 2) & 3);
+  else
+    // 64-byte rows (head_dim 32): chunk bit 1 = row bit 1 ^ row bit 3, chunk bit 0 = row bit 2
+    // (the same exhaustive search over row-bit XOR maps, against 32- and 64-bank models)
+    return ((((r >> 1) ^ (r >> 3)) & 1) << 1) | ((r >> 2) & 1);
 }
 
-// fp16 row sums per sub-tile (head_dim 64): 1 = a tree of packed fp16 adds over the rounded
+// fp16 row sums per sub-tile (head_dim 32 and 64): 1 = a tree of packed fp16 adds over the rounded
 // probabilities (then fp32 across sub-tiles), 0 = fp32 adds of the unrounded ones. The tree is 30 instructions
 // per 64 probabilities against 62 (measured +1.5% at C5, +3% at C3); its partial sums stay exact
 // to 2^-11 per level (each probability is <= 2^8, a sub-tile's 32 per lane sum to <= 2^13).
@@ -190,13 +194,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   static_assert(BLK % NW == 0 || NW % BLK == 0, "loader shape");
   // (head_dim 128 keeps fp32 sums: +0.6% there, and its context feeds the int8 re-quantisation
   // of the W8A8 block, where a larger context error moves more int8 codes)
-  constexpr bool SUM16 = MI355_ATTN_SUM16 && __is_same(T, _Float16) && HD == 64;
+  constexpr bool SUM16 = MI355_ATTN_SUM16 && __is_same(T, _Float16) && HD <= 64;
 
   // LDS ring of NSTAGE stages x KT sub-tiles, K and V both in their natural [key][hd] layout.
   // Without the look-ahead a wave reads one stage while the other is in flight (double
   // buffering); with it a wave may read V of sub-tile j and K of j+1 (two stages), so loads go
   // to the stage two ahead of a 3-stage ring.
-  constexpr int NSTAGE = PIPE ? 3 : (HD == 64 ? MI355_ATTN_NSTAGE64 : MI355_ATTN_NSTAGE128);
+  constexpr int NSTAGE = PIPE ? 3 : (HD <= 64 ? MI355_ATTN_NSTAGE64 : MI355_ATTN_NSTAGE128);
   __shared__ u32x4 k_lds[NSTAGE][KT][BN * KCH];
   __shared__ u32x4 v_lds[NSTAGE][KT][BN * KCH];
   // key-mask bytes of each sub-tile: a 1-byte LDS-DMA load writes each lane's byte
@@ -835,6 +839,13 @@ __global__ __launch_bounds__(64 * NWK) void attn_fwd_valu(AttnArgs p) {
 #ifndef MI355_ATTN_NW128
 #define MI355_ATTN_NW128 8
 #endif
+// head_dim 32: as head_dim 64 (4 waves of two 32-query groups, 32 KB of LDS per work-group)
+#ifndef MI355_ATTN_NW32
+#define MI355_ATTN_NW32 4
+#endif
+#ifndef MI355_ATTN_QG32
+#define MI355_ATTN_QG32 2
+#endif
 #ifndef MI355_ATTN_QG128
 #define MI355_ATTN_QG128 1
 #endif
@@ -871,9 +882,9 @@ __global__ __launch_bounds__(64 * NWK) void attn_fwd_valu(AttnArgs p) {
 
 template <typename T, int HD, int NW, int QG, bool CAUSAL, bool KMASK>
 void launch_one(const AttnArgs& a, dim3 grid, dim3 block, hipStream_t s) {
-  constexpr int KT = HD == 64 ? MI355_ATTN_KT64 : MI355_ATTN_KT128;
-  constexpr int WPE = HD == 64 ? MI355_ATTN_WPE64 : MI355_ATTN_WPE128;
-  constexpr bool PRIO = (HD == 64 ? MI355_ATTN_PRIO64 : MI355_ATTN_PRIO128) != 0;
+  constexpr int KT = HD <= 64 ? MI355_ATTN_KT64 : MI355_ATTN_KT128;
+  constexpr int WPE = HD <= 64 ? MI355_ATTN_WPE64 : MI355_ATTN_WPE128;
+  constexpr bool PRIO = (HD <= 64 ? MI355_ATTN_PRIO64 : MI355_ATTN_PRIO128) != 0;
   constexpr bool PIPE = HD == 64 && (!KMASK || MI355_ATTN_PIPE64 > 1) && MI355_ATTN_PIPE64 != 0;
   hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, KT, WPE, PRIO, PIPE, CAUSAL, KMASK>), grid, block, 0, s, a);
 }
@@ -1017,15 +1028,18 @@ extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const voi
   const bool cz = causal != 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == MI355_F32) return dispatch_valu<float>(a, head_dim, cz, kmask, s);
-  if (head_dim != 64 && head_dim != 128) {
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128) {
     return dtype == MI355_F16 ? dispatch_valu<_Float16>(a, head_dim, cz, kmask, s)
                               : dispatch_valu<__bf16>(a, head_dim, cz, kmask, s);
   }
   if (dtype == MI355_F16) {
+    if (head_dim == 32)
+      return launch_mfma<_Float16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, s);
     return head_dim == 64
                ? launch_mfma<_Float16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, s)
                : launch_mfma<_Float16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, s);
   }
+  if (head_dim == 32) return launch_mfma<__bf16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, s);
   return head_dim == 64
              ? launch_mfma<__bf16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, s)
              : launch_mfma<__bf16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, s);

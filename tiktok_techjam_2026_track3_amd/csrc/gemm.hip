@@ -585,20 +585,24 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
 #define MI355_GEMM_DIRECT 1
 #endif
 
-// Small fp32 problems (the fp32 configuration's projections are 128 x 768 x 256 and
-// 128 x 256 x 256): a 32 x 32 output tile per work-group whose NWS waves split K. With one wave
-// per tile a 32x32 fp32 MFMA tile costs K/2 MFMAs of 64 cycles in sequence; split NWS ways the
-// chain is NWS times shorter and NWS times more SIMDs share it. Fragments come straight from
+// Small problems (at most 512 tiles of 32 x 32 outputs: the fp32 configuration's projections
+// are 128 x 768 x 256 and 128 x 256 x 256; the official shapes' small batches), fp32 or 16-bit:
+// a 32 x 32 output tile per work-group whose NWS waves split K. With one wave per tile the
+// tile's MFMA chain (K/2 fp32 MFMAs, K/16 16-bit ones) runs in sequence; split NWS ways the
+// chain is NWS times shorter and NWS times more SIMDs share it, where a 256 x 256 tile would
+// leave all but a handful of CUs idle. Fragments come straight from
 // global memory (lane (l32, g) reads 16 bytes of row l32 for chunk 2j + g; rows are K-major),
 // U chunk pairs per wave requested before the first MFMA. The NWS partial tiles are summed
 // through LDS in wave order (deterministic), then bias, row mask and residual are applied per
 // element as in gemm_kernel's epilogue and the tile is written row by row.
-template <int NWS, bool GELU, bool LNF>
-__global__ __launch_bounds__(64 * NWS) void gemm_f32_splitk(GemmArgs p) {
+template <typename T, int NWS, bool GELU, bool LNF, typename TO>
+__global__ __launch_bounds__(64 * NWS) void gemm_splitk(GemmArgs p) {
   constexpr int U = 4;
   constexpr int PITCH = 65;  // padded: the reduction reads 32 features of one token per half-wave
   __shared__ float red[NWS][16][PITCH];
-  using MF = Mfma<float>;
+  using MF = Mfma<T>;
+  using frag = typename MF::frag;
+  constexpr int EPC = MF::ELEMS_PER_CHUNK;  // elements per 16-byte chunk
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int g = lane >> 5, l32 = lane & 31;
@@ -608,23 +612,25 @@ __global__ __launch_bounds__(64 * NWS) void gemm_f32_splitk(GemmArgs p) {
   const int64_t m0 = tmi * 32, n0 = tni * 32;
   const int64_t am = m0 + l32, wn = n0 + l32;
   const bool a_ok = am < p.M, w_ok = wn < p.N;
-  const float* arow = static_cast<const float*>(p.A) + (a_ok ? am : 0) * p.lda;
-  const float* wrow = static_cast<const float*>(p.W) + (w_ok ? wn : 0) * p.ldw;
-  const int nchunk = static_cast<int>(p.K / 4);
+  const T* arow = static_cast<const T*>(p.A) + (a_ok ? am : 0) * p.lda;
+  const T* wrow = static_cast<const T*>(p.W) + (w_ok ? wn : 0) * p.ldw;
+  const int nchunk = static_cast<int>(p.K / EPC);
 
   // D = W_rows . A_rows^T: lane l keeps token l % 32 and features mfma_row(i, l)
   typename MF::acc acc;
 #pragma unroll
   for (int i = 0; i < 16; ++i) acc[i] = 0.f;
-  // wave w takes chunk pairs w, w + NWS, w + 2 NWS, ...; half-wave g the pair's chunk g
+  // wave w takes chunk pairs w, w + NWS, w + 2 NWS, ...; half-wave g the pair's chunk g (A and W
+  // take the same chunk in every lane, so the MFMA's k order inside a pair does not matter)
   for (int base = 2 * wave; base < nchunk; base += 2 * NWS * U) {
-    f32x4 fa[U], fw[U];
+    frag fa[U], fw[U];
 #pragma unroll
     for (int u = 0; u < U; ++u) {
       const int c = base + u * 2 * NWS + g;
       const bool in = c < nchunk;
-      fa[u] = (in && a_ok) ? *reinterpret_cast<const f32x4*>(arow + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
-      fw[u] = (in && w_ok) ? *reinterpret_cast<const f32x4*>(wrow + 4 * c) : f32x4{0.f, 0.f, 0.f, 0.f};
+      const u32x4 zero = {0u, 0u, 0u, 0u};
+      fa[u] = __builtin_bit_cast(frag, (in && a_ok) ? *reinterpret_cast<const u32x4*>(arow + EPC * c) : zero);
+      fw[u] = __builtin_bit_cast(frag, (in && w_ok) ? *reinterpret_cast<const u32x4*>(wrow + EPC * c) : zero);
     }
 #pragma unroll
     for (int u = 0; u < U; ++u) acc = MF::mma(fw[u], fa[u], acc);
@@ -646,17 +652,20 @@ __global__ __launch_bounds__(64 * NWS) void gemm_f32_splitk(GemmArgs p) {
       v = ln_fold(v, p.ln_stats[2 * m], p.ln_stats[2 * m + 1], p.ln_colsum[n], p.bias ? p.bias[n] : 0.f);
     else if (p.bias)
       v = v + p.bias[n];
+    // the projection rounded to the output type first (a no-op for fp32), as in gemm_kernel
+    v = to_f32(from_f32<TO>(v));
     if constexpr (GELU) v = gelu_erf(v);
     const bool masked = p.row_valid && p.row_valid[m] == 0;
     if (masked) v = 0.f;
     // residual read before the write of the same element: R may be C
-    if (p.R) v = v + static_cast<const float*>(p.R)[m * p.ldr + n];
+    if (p.R) v = to_f32(from_f32<TO>(v)) + to_f32(static_cast<const TO*>(p.R)[m * p.ldr + n]);
     if (masked && (p.epi & EPI_ZERO_MASKED)) v = 0.f;
-    static_cast<float*>(p.C)[m * p.ldc + n] = v;
+    store_out<TO>(p.C, m * p.ldc + n, v);
   }
 }
 
-int launch_gemm_f32_splitk(const GemmArgs& a, hipStream_t stream) {
+template <typename T, typename TO>
+int launch_gemm_splitk(const GemmArgs& a, hipStream_t stream) {
   constexpr int NWS = 8;
   const int64_t tiles = ((a.M + 31) / 32) * ((a.N + 31) / 32);
   const dim3 grid(static_cast<unsigned>(tiles)), block(64 * NWS);
@@ -664,17 +673,21 @@ int launch_gemm_f32_splitk(const GemmArgs& a, hipStream_t stream) {
   // epilogue slowed every projection by ~10%
   const bool lnf = a.ln_stats != nullptr;
   if (a.epi & EPI_GELU) {
-    if (lnf) hipLaunchKernelGGL((gemm_f32_splitk<NWS, true, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((gemm_f32_splitk<NWS, true, false>), grid, block, 0, stream, a);
+    if (lnf) hipLaunchKernelGGL((gemm_splitk<T, NWS, true, true, TO>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((gemm_splitk<T, NWS, true, false, TO>), grid, block, 0, stream, a);
   } else {
-    if (lnf) hipLaunchKernelGGL((gemm_f32_splitk<NWS, false, true>), grid, block, 0, stream, a);
-    else hipLaunchKernelGGL((gemm_f32_splitk<NWS, false, false>), grid, block, 0, stream, a);
+    if (lnf) hipLaunchKernelGGL((gemm_splitk<T, NWS, false, true, TO>), grid, block, 0, stream, a);
+    else hipLaunchKernelGGL((gemm_splitk<T, NWS, false, false, TO>), grid, block, 0, stream, a);
   }
   return static_cast<int>(hipGetLastError());
 }
 
 template <typename T, typename TO, int BM, int BN, int WM, int WN, bool INT8>
 int launch_gemm(const GemmArgs& a, hipStream_t stream) {
+  if constexpr (!INT8 && sizeof(T) == 2) {
+    // small 16-bit problems: the split-K kernel (see gemm_splitk)
+    if (((a.M + 31) / 32) * ((a.N + 31) / 32) <= 512) return launch_gemm_splitk<T, TO>(a, stream);
+  }
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (tiles <= 0) return MI355_OK;
   if (tiles > 0x7fffffffLL) return MI355_E_BAD_SIZE;
@@ -755,7 +768,9 @@ int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, cons
   const bool ok_in = in_dtype == MI355_F32 || in_dtype == MI355_F16 || in_dtype == MI355_BF16;
   const bool ok_out = out_dtype == MI355_F32 || out_dtype == MI355_F16 || out_dtype == MI355_BF16;
   if (!ok_in || !ok_out) return MI355_E_BAD_DTYPE;
-  if ((in_dtype == MI355_F32) != (out_dtype == MI355_F32)) return MI355_E_UNSUPPORTED;
+  // fp32 inputs give fp32 or fp16 (the attention core type of an fp32 model's fp16 core);
+  // 16-bit inputs give either 16-bit type or fp32
+  if (in_dtype == MI355_F32 && out_dtype == MI355_BF16) return MI355_E_UNSUPPORTED;
   const int64_t epc = in_dtype == MI355_F32 ? 4 : 8;
   if (K % epc || lda % epc || ldw % epc || !aligned16(A) || !aligned16(W))
     return MI355_E_ALIGNMENT;
@@ -787,7 +802,12 @@ int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, cons
       // 32 x 32 tiles with K split over 8 waves; mid-size ones 64 x 64 tiles
       const int64_t tiles32 = ((a.M + 31) / 32) * ((a.N + 31) / 32);
       const int64_t tiles128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
-      if (tiles32 <= 512) return launch_gemm_f32_splitk(a, s);
+      if (out_dtype == MI355_F16) {
+        if (tiles32 <= 512) return launch_gemm_splitk<float, _Float16>(a, s);
+        if (tiles128 < 64) return launch_gemm<float, _Float16, 64, 64, 2, 2, false>(a, s);
+        return launch_gemm<float, _Float16, 128, 128, 2, 2, false>(a, s);
+      }
+      if (tiles32 <= 512) return launch_gemm_splitk<float, float>(a, s);
       if (tiles128 < 64) return launch_gemm<float, float, 64, 64, 2, 2, false>(a, s);
       return launch_gemm<float, float, 128, 128, 2, 2, false>(a, s);
     }

@@ -51,8 +51,8 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
     """``out[M, N] = x[M, K] @ weight[N, K]^T + bias[N]`` (nn.Linear), fp32 accumulate.
 
     ``x`` may be a row-strided 2-D view (unit column stride); ``weight`` must be contiguous and
-    of x's dtype; ``bias`` is fp32. ``out_dtype`` (default x's dtype) may be the other 16-bit
-    type for 16-bit inputs. Rows whose ``row_valid`` entry is False are written as zeros.
+    of x's dtype; ``bias`` is fp32. ``out_dtype`` (default x's dtype) may be any of fp32 /
+    fp16 / bf16 for 16-bit inputs, and fp32 or fp16 for fp32 inputs. Rows whose ``row_valid`` entry is False are written as zeros.
     With ``residual`` ([M, N] of out_dtype, unit column stride; may be ``out`` itself) the result
     is ``residual + out_dtype(projection)``, masked rows giving ``residual`` -- or zeros with
     ``zero_masked_rows`` (the block's trailing masked_fill). ``gelu`` applies the exact GELU to
@@ -170,8 +170,8 @@ def layernorm_linear(x: torch.Tensor, weight: torch.Tensor, colsum: torch.Tensor
     """``nn.Linear(nn.LayerNorm(x))`` (optionally followed by the exact GELU) without writing the
     normalised rows: ``weight``, ``colsum`` and ``bias`` come from ``fold_layernorm``. ``x`` is a
     2-D row-strided tensor (unit column stride); the row statistics go to ``stats`` ([M, 2] fp32
-    workspace, allocated when not given). ``out_dtype`` defaults to x's dtype (a bf16 input may
-    give fp16)."""
+    workspace, allocated when not given). ``out_dtype`` defaults to x's dtype (a bf16 or fp32
+    input may give fp16)."""
     _on_gpu(x, weight, colsum, bias, out, stats)
     if x.dim() != 2 or weight.dim() != 2 or x.stride(1) != 1:
         raise ValueError("layernorm_linear expects a 2-D x with unit column stride and 2-D weight")
