@@ -108,6 +108,11 @@ MI355_DEVINL int swz(int r) {
 #ifndef MI355_ATTN_SUM16
 #define MI355_ATTN_SUM16 1
 #endif
+// the sub-tile's masking decision taken before its score MFMAs (see stage): 1 = causal instances
+// (C3 +5%), 2 = all (the unmasked head_dim-64 instance then spills and runs 0.6% slower), 0 = none
+#ifndef MI355_ATTN_SPLITMAX
+#define MI355_ATTN_SPLITMAX 1
+#endif
 
 template <typename T>
 MI355_DEVINL typename Mfma<T>::frag pack8(const float* p) {
@@ -195,6 +200,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   // (head_dim 128 keeps fp32 sums: +0.6% there, and its context feeds the int8 re-quantisation
   // of the W8A8 block, where a larger context error moves more int8 codes)
   constexpr bool SUM16 = MI355_ATTN_SUM16 && __is_same(T, _Float16) && HD <= 64;
+  constexpr bool SPLITMAX = MI355_ATTN_SPLITMAX == 2 || (MI355_ATTN_SPLITMAX == 1 && CAUSAL);
 
   // LDS ring of NSTAGE stages x KT sub-tiles, K and V both in their natural [key][hd] layout.
   // Without the look-ahead a wave reads one stage while the other is in flight (double
@@ -379,41 +385,47 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   };
 
   // masks and the lazy running max of sub-tile j; returns after any O/l/mu update
-  auto softmax_max = [&](f32x16 (&sacc)[QG][2], const int j, const int st, const int k) MI355_LAMBDA_INLINE {
+  // whether sub-tile j needs element masking for this wave (key mask, sequence end, causal
+  // diagonal; wave-uniform); vbits receives the tile's key-mask validity word
+  auto tile_masked = [&](const int j, const int st, const int k, uint64_t& vbits) MI355_LAMBDA_INLINE {
     const int k0 = j * BN;
     // tile validity word: bit kk set <=> key k0 + kk is valid under the key mask
-    uint64_t vbits = ~0ull;
+    vbits = ~0ull;
     if constexpr (KMASK) vbits = __builtin_amdgcn_ballot_w64(kv_lds[st][k][lane] != 0);
-    const bool need_mask =
-        (vbits != ~0ull) || (k0 + BN > Sk) || (CAUSAL && k0 + BN - 1 > q_wave32);
-    if (need_mask) {
-      // one validity word per lane: key mask, sequence end and (causal) the query's diagonal;
-      // shifted by the lane's 4g offset, element (t, i) is bit 32t + 8(i/4) + i%4 -- a
-      // compile-time position, so no per-element shift amounts stay live in registers
-      const int rem = Sk - k0;  // keys left in the sequence (> 0 for an issued sub-tile)
-      uint64_t w = vbits;
-      if (rem < BN) w &= (1ull << rem) - 1ull;
-#pragma unroll
-      for (int n = 0; n < QG; ++n) {
-        uint64_t wn = w;
-        if constexpr (CAUSAL) {
-          const int lim = q_wave32 + 32 * n + l32 - k0 + 1;  // keys kk < lim are allowed
-          wn &= lim >= BN ? ~0ull : (lim <= 0 ? 0ull : ((1ull << lim) - 1ull));
-        }
-        const uint64_t wl = wn >> (4 * g);
-        const uint32_t half[2] = {static_cast<uint32_t>(wl), static_cast<uint32_t>(wl >> 32)};
-#pragma unroll
-        for (int t = 0; t < 2; ++t)
-#pragma unroll
-          for (int i = 0; i < 16; ++i) {
-            const uint32_t bit = 1u << (8 * (i / 4) + (i % 4));
-            if (!(half[t] & bit)) sacc[n][t][i] = NEG_INF;
-          }
-      }
-    }
+    return (vbits != ~0ull) || (k0 + BN > Sk) || (CAUSAL && k0 + BN - 1 > q_wave32);
+  };
+  // -inf on the masked scores of sub-tile j
+  auto mask_scores = [&](f32x16 (&sacc)[QG][2], const int j, const uint64_t vbits) MI355_LAMBDA_INLINE {
+    const int k0 = j * BN;
+    // one validity word per lane: key mask, sequence end and (causal) the query's diagonal;
+    // shifted by the lane's 4g offset, element (t, i) is bit 32t + 8(i/4) + i%4 -- a
+    // compile-time position, so no per-element shift amounts stay live in registers
+    const int rem = Sk - k0;  // keys left in the sequence (> 0 for an issued sub-tile)
+    uint64_t w = vbits;
+    if (rem < BN) w &= (1ull << rem) - 1ull;
 #pragma unroll
     for (int n = 0; n < QG; ++n) {
-      // two v_maximum3 chains of 16 scores (NaN-propagating maximum: no operand quieting)
+      uint64_t wn = w;
+      if constexpr (CAUSAL) {
+        const int lim = q_wave32 + 32 * n + l32 - k0 + 1;  // keys kk < lim are allowed
+        wn &= lim >= BN ? ~0ull : (lim <= 0 ? 0ull : ((1ull << lim) - 1ull));
+      }
+      const uint64_t wl = wn >> (4 * g);
+      const uint32_t half[2] = {static_cast<uint32_t>(wl), static_cast<uint32_t>(wl >> 32)};
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const uint32_t bit = 1u << (8 * (i / 4) + (i % 4));
+          if (!(half[t] & bit)) sacc[n][t][i] = NEG_INF;
+        }
+    }
+  };
+  // row maxima of a sub-tile's scores: two v_maximum3 chains of 16 scores per query group
+  // (NaN-propagating maximum: no operand quieting) and one lane-pair exchange
+  auto row_max = [&](f32x16 (&sacc)[QG][2], float (&mx)[QG]) MI355_LAMBDA_INLINE {
+#pragma unroll
+    for (int n = 0; n < QG; ++n) {
       float m2[2];
 #pragma unroll
       for (int t = 0; t < 2; ++t) {
@@ -422,12 +434,21 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
         for (int i = 2; i < 16; ++i) m = vmax(m, sacc[n][t][i]);
         m2[t] = m;
       }
-      const float mx = pair_maximum(vmax(m2[0], m2[1]));
-      // move mu only when the tile max exceeds it by more than thr, or on the first finite
-      // tile (gate is -inf until then)
-      const bool grow = mx > gate[n];
+      mx[n] = pair_maximum(vmax(m2[0], m2[1]));
+    }
+  };
+  // the lazy running max: move mu only when the tile max exceeds it by more than thr, or on the
+  // first finite tile (gate is -inf until then); one wave-wide test for all query groups
+  auto lazy_rescale = [&](f32x16 (&sacc)[QG][2], const float (&mx)[QG]) MI355_LAMBDA_INLINE {
+    bool any = false;
+#pragma unroll
+    for (int n = 0; n < QG; ++n) any = any || mx[n] > gate[n];
+    if (__builtin_amdgcn_ballot_w64(any) == 0) return;
+#pragma unroll
+    for (int n = 0; n < QG; ++n) {
+      const bool grow = mx[n] > gate[n];
       if (__builtin_amdgcn_ballot_w64(grow) != 0) {
-        const float shift = grow ? mx : 0.f;
+        const float shift = grow ? mx[n] : 0.f;
         const float alpha = gate[n] == NEG_INF ? 1.f : fast_exp2(-shift);
         lsum[n] *= alpha;
 #pragma unroll
@@ -443,6 +464,14 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
         gate[n] = grow ? thr : gate[n];
       }
     }
+  };
+  // masks and the lazy running max of sub-tile j; returns after any O/l/mu update
+  auto softmax_max = [&](f32x16 (&sacc)[QG][2], const int j, const int st, const int k) MI355_LAMBDA_INLINE {
+    uint64_t vbits;
+    if (tile_masked(j, st, k, vbits)) mask_scores(sacc, j, vbits);
+    float mx[QG];
+    row_max(sacc, mx);
+    lazy_rescale(sacc, mx);
   };
 
   // probabilities of sub-tile j and O^T (hd x QW) += V^T (hd x 64 keys) . P^T (64 keys x QW)
@@ -561,8 +590,25 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
         }
       } else {
         if (j < n_kt && active(j)) {
-          score(s_a, cur, k);
-          softmax_max(s_a, j, cur, k);
+          if constexpr (SPLITMAX) {
+            // the masking decision first, so that in the common unmasked case the score MFMAs
+            // and the row maxima share one basic block and the maxima of the first 32 keys can
+            // issue while the MFMAs of the second 32 run
+            uint64_t vbits;
+            float mx[QG];
+            if (tile_masked(j, cur, k, vbits)) {
+              score(s_a, cur, k);
+              mask_scores(s_a, j, vbits);
+              row_max(s_a, mx);
+            } else {
+              score(s_a, cur, k);
+              row_max(s_a, mx);
+            }
+            lazy_rescale(s_a, mx);
+          } else {
+            score(s_a, cur, k);
+            softmax_max(s_a, j, cur, k);
+          }
           exp_pv(s_a, cur, k);
         }
       }
