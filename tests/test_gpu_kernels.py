@@ -163,6 +163,23 @@ def test_attention_packed_qkv_views(gpu, dtype, causal):
     _attn_check(gpu, dtype, 2, 4, 333, 333, 64, causal, packed=True, seed=11)
 
 
+@pytest.mark.parametrize("hd", [32, 64, 128])
+def test_attention_output_rows_8_byte_aligned(gpu, hd):
+    """Output rows that are only 8-byte aligned (a view 4 fp16 elements into its buffer) take
+    the direct 8-byte stores instead of the LDS-staged 16-byte row chunks; both give the same
+    bits."""
+    ops = _ops()
+    B, S, H = 2, 300, 2
+    q, k, v = (_rand((B, S, H, hd), torch.float16, 70 + i).to(gpu) for i in range(3))
+    aligned = ops.attention(q, k, v, scale=hd ** -0.5)
+    buf = torch.full((B * S * H * hd + 4,), float("nan"), dtype=torch.float16, device=gpu)
+    shifted = buf[4:].view(B, S, H, hd)
+    assert shifted.data_ptr() % 16 == 8
+    ops.attention(q, k, v, out=shifted, scale=hd ** -0.5)
+    assert torch.equal(shifted, aligned)
+    assert torch.isnan(buf[:4]).all()
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 def test_attention_rectangular_and_large_scores(gpu, dtype):
     _attn_check(gpu, dtype, 1, 2, 100, 700, 64, False, seed=21)
