@@ -272,6 +272,75 @@ def test_layernorm_linear_rejects_bad_arguments(gpu):
         ops.layernorm_linear(x[:, :60], w[:, :60].contiguous(), cs, b)   # K not a multiple of 8
 
 
+# ------------------------------------------------------------------ persistent GEMM tiles
+def _persistent_shape(gpu, N, K):
+    """M such that the [M, N] output has more than twice as many 256 x 256 tiles as the device
+    has CUs (with K <= 512 the persistent launch: each work-group loops over tiles, prefetches
+    the next tile's first K step and stores from registers), with a partial last row tile; and
+    the row-slice length whose slices have at most as many tiles as CUs (one tile per
+    work-group)."""
+    ncu = torch.cuda.get_device_properties(gpu).multi_processor_count
+    cols = (N + 255) // 256
+    per_slice = max(1, ncu // cols)
+    M = 256 * (2 * per_slice + 8) + 37
+    assert ((M + 255) // 256) * cols > 2 * ncu and per_slice * cols <= ncu
+    return M, 256 * per_slice
+
+
+@pytest.mark.parametrize("dtype,odt", [(torch.float16, torch.float16), (torch.bfloat16, torch.bfloat16),
+                                       (torch.float16, torch.float32), (torch.bfloat16, torch.float16),
+                                       (torch.float16, torch.bfloat16)])
+@pytest.mark.parametrize("epi", ["plain", "residual", "zero_masked", "gelu", "layernorm"])
+def test_linear_persistent_tiles_match_single_pass(gpu, dtype, odt, epi):
+    """A projection with more tiles than CUs (persistent work-groups) equals, bit for bit, the
+    same projection computed on row slices that each take one tile per work-group: same MFMA
+    accumulation order, same epilogue arithmetic. N = 1544 leaves an 8-feature last tile
+    column; K = 512 and 256 are whole turns of the 2-slot K ring. Every epilogue: bias, residual
+    with masked rows kept or zeroed, GELU, the folded LayerNorm (its output types)."""
+    from tiktok_techjam_2026_track3_amd import ops
+    if epi == "layernorm" and (dtype, odt) not in LNF_TYPES:
+        pytest.skip("the LayerNorm fold gives the input type or fp16")
+    N, K = 1544, (256 if epi == "gelu" else 512)
+    M, step = _persistent_shape(gpu, N, K)
+    print(f"persistent linear {dtype}->{odt} epi={epi} M={M} N={N} K={K} slice={step}", flush=True)
+    g = torch.Generator().manual_seed(N + K + len(epi))
+    x = torch.randn(M, K, generator=g).to(dtype).to(gpu)
+    x[1::5] += 3.0
+    wt = (torch.randn(N, K, generator=g) * K ** -0.5).to(dtype).to(gpu)
+    b = torch.randn(N, generator=g).to(gpu)
+    r = (torch.randn(M, N, generator=g) * 2).to(odt).to(gpu)
+    valid = (torch.rand(M, generator=g) > 0.25).to(gpu)
+    if epi == "layernorm":
+        gamma = (1 + 0.3 * torch.randn(K, generator=g)).to(dtype).to(gpu)
+        beta = (0.2 * torch.randn(K, generator=g)).to(dtype).to(gpu)
+        wf, colsum, bf = ops.fold_layernorm(wt, b, gamma, beta, dtype)
+
+    def run(rows):
+        if epi == "plain":
+            return ops.linear(x[rows], wt, b, out_dtype=odt)
+        if epi == "residual":
+            return ops.linear(x[rows], wt, b, out_dtype=odt, residual=r[rows], row_valid=valid[rows])
+        if epi == "zero_masked":
+            return ops.linear(x[rows], wt, b, out_dtype=odt, residual=r[rows], row_valid=valid[rows],
+                              zero_masked_rows=True)
+        if epi == "gelu":
+            return ops.linear(x[rows], wt, b, out_dtype=odt, gelu=True)
+        return ops.layernorm_linear(x[rows], wf, colsum, bf, 1e-5, out_dtype=odt)
+
+    whole = run(slice(0, M))
+    parts = torch.cat([run(slice(r0, min(M, r0 + step))) for r0 in range(0, M, step)])
+    torch.cuda.synchronize()
+    same = whole == parts
+    assert bool(same.all()), f"{int((~same).sum())} elements differ"
+    if epi == "plain":
+        # and within the GEMM bound against fp64 on a sample of rows (incl. the partial tile)
+        rows = torch.cat([torch.arange(0, 300), torch.arange(M - 300, M)])
+        a64, w64 = x[rows].cpu().double(), wt.cpu().double()
+        ref = a64 @ w64.T + b.cpu().double()
+        bound = UNIT_OF[odt] * ref.abs() + 4 * K * 2.0 ** -24 * (a64.abs() @ w64.abs().T) + 1e-7
+        assert bool(((whole[rows].cpu().double() - ref).abs() <= bound).all())
+
+
 @pytest.mark.parametrize("seed", SEEDS)
 @pytest.mark.parametrize("name", ["C1", "C2", "C3"])
 def test_attention_half_matches_oracle(gpu, name, seed):
