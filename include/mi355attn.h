@@ -91,6 +91,33 @@ int mi355_attn_fwd(int dtype, const void* Q, const void* K, const void* V, void*
                    int64_t key_valid_sb, void* stream);
 
 /*
+ * mi355_attn_fwd with a caller-provided workspace (same interface and results contract; replaces
+ * the same reference code). On the matrix-core kernel (F16 / BF16, head_dim 32, 64, 128) a
+ * workspace of at least B * H * ceil(S_k / 1024) * 4 bytes (4-byte aligned) holds the key-norm
+ * bounds max |k| per 1024-key chunk of every head, computed by a pass over K on the same stream
+ * before the attention launch. A wave whose every query satisfies |c q| max|k| - mu <= 8 (c =
+ * scale * log2 e, mu its lazily moved running maximum) can never move mu again, so it skips the
+ * per-tile row maxima for the rest of its sweep: the output is bit-identical to mi355_attn_fwd.
+ * workspace may be NULL (then the same as mi355_attn_fwd); a smaller non-NULL workspace is
+ * MI355_E_BAD_SIZE. Causal calls with a key mask do not use it. The workspace is scratch: its
+ * contents on return are unspecified, and calls that share one workspace must be stream-ordered.
+ */
+int mi355_attn_fwd_ws(int dtype, const void* Q, const void* K, const void* V, void* O, int64_t B,
+                      int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim,
+                      const int64_t* q_strides, const int64_t* k_strides,
+                      const int64_t* v_strides, const int64_t* o_strides, float scale,
+                      int causal, const uint8_t* key_valid, int64_t key_valid_sb,
+                      void* workspace, int64_t workspace_bytes, void* stream);
+
+/*
+ * Workspace bytes the library recommends for mi355_attn_fwd_ws on this problem: the key-norm
+ * bound size when the problem runs on the matrix-core kernel with S_k >= 32768 (shorter key
+ * ranges do not repay the extra pass over K), else 0 (call without a workspace).
+ */
+int64_t mi355_attn_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t S_q, int64_t S_k,
+                                   int64_t head_dim);
+
+/*
  * Per-row symmetric int8 quantisation of X[M,K] (row stride ldx) into Xq[M,K] (contiguous) and
  * scale[M] (fp32). mode 0 = activation recipe `_quant_rows`
  * (Project/kernels/k008_int8_gemm.py:148-151): s = max(amax, 1e-6) / 127.

@@ -126,6 +126,37 @@ def test_attention_argument_validation():
     assert call(B=0) == 0
 
 
+def test_attention_workspace_argument_validation():
+    """mi355_attn_fwd_ws: the recommended size is the key-norm bound array of the matrix-core
+    kernel (B * H * ceil(S_k / 1024) floats) from S_k = 32768 on, 0 elsewhere; a non-NULL
+    workspace below the bound size or misaligned is refused before any launch."""
+    L = _lib()
+    h = L.lib()
+    codes = _status_codes()
+    fake = 1 << 20
+    B, H = 2, 4
+    assert h.mi355_attn_workspace_bytes(1, B, H, 32768, 32768, 64) == B * H * 32 * 4
+    assert h.mi355_attn_workspace_bytes(2, B, H, 10, 100000, 128) == B * H * 98 * 4
+    assert h.mi355_attn_workspace_bytes(1, B, H, 40000, 40000, 32) == B * H * 40 * 4
+    assert h.mi355_attn_workspace_bytes(1, B, H, 8192, 8192, 64) == 0      # short key range
+    assert h.mi355_attn_workspace_bytes(0, B, H, 8192, 8192, 64) == 0      # fp32: VALU kernel
+    assert h.mi355_attn_workspace_bytes(1, B, H, 8192, 8192, 80) == 0      # head_dim 80: VALU
+    S = 3000  # 3 chunks
+    st = L.i64_array((3 * 64 * H * S, 3 * 64 * H, 64))
+    ost = L.i64_array((64 * H * S, 64 * H, 64))
+
+    def call(ws, nbytes):
+        return h.mi355_attn_fwd_ws(1, fake, fake, fake, fake, B, H, S, S, 64, st, st, st, ost,
+                                   0.125, 0, None, 0, ws, nbytes, None)
+
+    need = B * H * 3 * 4
+    assert call(fake, need - 4) == codes["MI355_E_BAD_SIZE"]
+    assert call(fake + 2, need) == codes["MI355_E_ALIGNMENT"]
+    # argument validation still precedes the workspace check
+    assert h.mi355_attn_fwd_ws(1, fake, fake, fake, fake, B, H, S, S, 40, st, st, st, ost, 0.125, 0,
+                               None, 0, fake, need, None) == codes["MI355_E_HEAD_DIM"]
+
+
 def test_int8_argument_validation():
     L = _lib()
     h = L.lib()

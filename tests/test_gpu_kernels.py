@@ -100,10 +100,11 @@ def test_linear_rejects_bad_arguments(gpu):
 
 
 # ---------------------------------------------------------------------------- attention
-def _attn_check(gpu, dtype, B, H, Sq, Sk, hd, causal, key_valid=None, packed=False, seed=0, qscale=1.0):
+def _attn_check(gpu, dtype, B, H, Sq, Sk, hd, causal, key_valid=None, packed=False, seed=0, qscale=1.0,
+                key_bound=None, kscale=1.0):
     ops = _ops()
     print(f"attention dtype={dtype} B={B} H={H} Sq={Sq} Sk={Sk} hd={hd} causal={causal} "
-          f"mask={key_valid is not None} packed={packed}", flush=True)
+          f"mask={key_valid is not None} packed={packed} key_bound={key_bound}", flush=True)
     if packed:
         assert Sq == Sk
         qkv = _rand((B, Sq, 3, H, hd), dtype, seed)
@@ -113,11 +114,12 @@ def _attn_check(gpu, dtype, B, H, Sq, Sk, hd, causal, key_valid=None, packed=Fal
         gq, gk, gv = g_qkv[:, :, 0], g_qkv[:, :, 1], g_qkv[:, :, 2]
     else:
         q = _rand((B, Sq, H, hd), dtype, seed, scale=qscale)
-        k = _rand((B, Sk, H, hd), dtype, seed + 1)
+        k = _rand((B, Sk, H, hd), dtype, seed + 1, scale=kscale)
         v = _rand((B, Sk, H, hd), dtype, seed + 2)
         gq, gk, gv = q.to(gpu), k.to(gpu), v.to(gpu)
     kv = None if key_valid is None else key_valid.to(gpu)
-    out = ops.attention(gq, gk, gv, scale=hd ** -0.5, causal=causal, key_valid=kv).cpu().double()
+    out = ops.attention(gq, gk, gv, scale=hd ** -0.5, causal=causal, key_valid=kv,
+                        key_bound=key_bound).cpu().double()
     tq, tk, tv = (t.double().transpose(1, 2) for t in (q, k, v))
     ref = OA.attention_core(tq, tk, tv, hd ** -0.5, causal, key_valid).transpose(1, 2)
     pav = OA.attention_core(tq, tk, tv.abs(), hd ** -0.5, causal, key_valid).transpose(1, 2)
@@ -345,3 +347,81 @@ def test_attention_key_mask_repeatable(gpu, dtype):
         if first is None:
             first = o
         assert torch.equal(o, first), f"run {rep} differs from run 0"
+
+
+# ------------------------------------------------------------- key-norm bound (workspace path)
+def _bound_pair(gpu, dtype, B, H, S, hd, causal, scale_qk, seed, key_valid=None, packed=False):
+    """The same problem through mi355_attn_fwd (exact row maxima on every tile) and
+    mi355_attn_fwd_ws (key-norm bounds); returns both outputs and the inputs."""
+    ops = _ops()
+    if packed:
+        qkv = _rand((B, S, 3, H, hd), dtype, seed, scale=scale_qk).to(gpu)
+        q, k, v = qkv[:, :, 0], qkv[:, :, 1], qkv[:, :, 2]
+    else:
+        q = _rand((B, S, H, hd), dtype, seed, scale=scale_qk).to(gpu)
+        k = _rand((B, S, H, hd), dtype, seed + 1, scale=scale_qk).to(gpu)
+        v = _rand((B, S, H, hd), dtype, seed + 2).to(gpu)
+    kv = None if key_valid is None else key_valid.to(gpu)
+    a = ops.attention(q, k, v, causal=causal, key_valid=kv, key_bound=False)
+    b = ops.attention(q, k, v, causal=causal, key_valid=kv, key_bound=True)
+    return a.cpu(), b.cpu()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hd", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("S,scale_qk", [(100, 1.0), (1500, 1.0), (2600, None), (1100, 3.0)])
+def test_attention_key_bound_bit_identical(gpu, dtype, hd, causal, S, scale_qk):
+    """mi355_attn_fwd_ws skips a wave's row maxima only once the key-norm bound shows that its
+    running max can never move again, so its output equals the exact path's bit for bit: on
+    Q, K ~ N(0,1)/sqrt(head_dim) (the C5 core distribution: the bound holds after the first tile),
+    N(0,1) (it holds for few waves) and large scores (never)."""
+    sc = hd ** -0.5 if scale_qk is None else scale_qk
+    print(f"key bound dtype={dtype} hd={hd} causal={causal} S={S} scale={sc}", flush=True)
+    a, b = _bound_pair(gpu, dtype, 2, 3, S, hd, causal, sc, 41)
+    assert torch.equal(torch.isnan(a), torch.isnan(b)) and not torch.isnan(a).any()
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+def test_attention_key_bound_against_oracle(gpu, dtype):
+    """The workspace path against the oracle under the exact path's error bound (C5 core
+    distribution, where it skips the row maxima after the first tile)."""
+    _attn_check(gpu, dtype, 2, 3, 2600, 2600, 64, False, seed=45, qscale=0.125, kscale=0.125,
+                key_bound=True)
+    _attn_check(gpu, dtype, 2, 3, 2600, 2600, 32, True, seed=46, qscale=32 ** -0.5,
+                kscale=32 ** -0.5, key_bound=True)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_key_bound_masked_packed(gpu, dtype, causal):
+    B, S = 2, 1300
+    g = torch.Generator().manual_seed(9)
+    mask = torch.rand(B, S, generator=g) > 0.2
+    mask[:, 0] = True
+    mask[1] = torch.arange(S) < 900
+    a, b = _bound_pair(gpu, dtype, B, 2, S, 64, causal, 0.125, 47, key_valid=mask)
+    assert torch.equal(a, b)
+    a, b = _bound_pair(gpu, dtype, B, 2, S, 64, causal, 0.125, 48, packed=True)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("bad", [float("nan"), float("inf"), 3.0e4])
+def test_attention_key_bound_nonfinite_and_huge_keys(gpu, bad):
+    """A NaN / inf / huge key makes the bound of its head non-finite or loose: that head runs
+    the exact path, bit for bit (NaN where it gives NaN); the other heads are unaffected."""
+    ops = _ops()
+    dtype = torch.float16
+    B, S, H, hd = 1, 2100, 2, 64
+    q = _rand((B, S, H, hd), dtype, 61, scale=0.125).to(gpu)
+    k = _rand((B, S, H, hd), dtype, 62, scale=0.125)
+    k[0, 1234, 1, 5] = bad
+    k = k.to(gpu)
+    v = _rand((B, S, H, hd), dtype, 63).to(gpu)
+    a = ops.attention(q, k, v, key_bound=False).cpu()
+    b = ops.attention(q, k, v, key_bound=True).cpu()
+    assert torch.equal(torch.isnan(a), torch.isnan(b))
+    fin = ~torch.isnan(a)
+    assert torch.equal(a[fin], b[fin])
+    assert torch.isfinite(a[:, :, 0]).all()

@@ -34,6 +34,13 @@ _SIGNATURES = {
          C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64),
          C.c_float, C.c_int, _P, _I64, _P],
     ),
+    "mi355_attn_workspace_bytes": (_I64, [C.c_int, _I64, _I64, _I64, _I64, _I64]),
+    "mi355_attn_fwd_ws": (
+        C.c_int,
+        [C.c_int, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
+         C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64),
+         C.c_float, C.c_int, _P, _I64, _P, _I64, _P],
+    ),
     "mi355_quant_rows_i8": (C.c_int, [C.c_int, _P, _I64, _P, _P, _I64, _I64, C.c_int, _P]),
     "mi355_layernorm": (C.c_int, [C.c_int, _P, _I64, _P, _P, C.c_float, _P, _I64, _I64, _I64, _P]),
     "mi355_gemm_bias_residual": (

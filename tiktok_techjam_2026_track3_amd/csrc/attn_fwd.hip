@@ -19,7 +19,11 @@
 //   * the running max mu is only moved when a tile's max exceeds it by more than 8, so the O/l
 //     rescale is skipped on most tiles; unnormalised probabilities stay <= 2^8;
 //   * causal work-groups stop at the diagonal, mask only tiles that cross it, and are issued
-//     longest-first.
+//     longest-first;
+//   * with key-norm bounds (attn_key_bound: max |k| of the head's keys) a wave whose every
+//     query satisfies |c q| max|k| - mu <= 8 (Cauchy-Schwarz: no later score can exceed the lazy
+//     threshold, so mu can never move again) skips the row maxima and the rescale test for the
+//     rest of its sweep, with bit-identical results.
 // fp32 kernel: one query per lane on VALU (the fp32 configuration is launch-latency bound).
 #include "common.h"
 
@@ -40,7 +44,18 @@ struct AttnArgs {
   int64_t kv_sb;
   int n_qtiles;
   int o_vec;  // output base and strides keep every output row 16-byte aligned
+  // key-norm bounds (nullable; MFMA kernel): kb[(b * H + h) * kb_n + i] = max |k| over key chunk
+  // i of head (b, h), written by attn_key_bound
+  const float* kb;
+  int kb_n;
 };
+
+// Keys per chunk of the key-norm bound pass.
+constexpr int KB_CHUNK = 1024;
+
+// MFMA kernel instances that take key-norm bounds
+template <bool PIPE, bool CAUSAL, bool KMASK>
+constexpr bool KB_INSTANCE = !PIPE && !(CAUSAL && KMASK);
 
 constexpr float NEG_INF = -__builtin_huge_valf();
 
@@ -252,6 +267,41 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
     }
   }
 
+  // Key-norm bound of this head: kmax = max |k| over its keys (wave-uniform). With it, no score
+  // s*c of query q can exceed |qf_q| kmax (Cauchy-Schwarz on the rounded operands the MFMAs
+  // multiply; the fp32 accumulation error, <= 2^-17 of that product, is covered by the margin
+  // in qbound).
+  // The query norms |qf| wait in LDS for the rare rescale branch that reads them (held in
+  // registers, or recomputed there, they stay live across the sweep: the loop-invariant code is
+  // hoisted).
+  // (not in the causal key-masked instances: at head_dim 64 the bound test takes them past the
+  // register budget; the host passes no bounds to them)
+  const bool use_kb = KB_INSTANCE<PIPE, CAUSAL, KMASK> && p.kb != nullptr;
+  __shared__ float qn_lds[QG][NT];
+  float kmax = 0.f;
+  if (use_kb) {
+#pragma unroll
+    for (int n = 0; n < QG; ++n) {
+      float ss = 0.f;
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const float v = to_f32(qf[n][s][r]);
+          ss = __builtin_fmaf(v, v, ss);
+        }
+      qn_lds[n][tid] = __builtin_sqrtf(pair_sum(ss));
+    }
+    const float* kbp = p.kb + (b * p.H + h) * p.kb_n;
+    float m = 0.f;
+    for (int i = lane; i < p.kb_n; i += 64) m = vmax(m, kbp[i]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = vmax(m, __shfl_xor(m, off));
+    kmax = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m)));
+  }
+  // set once every query of the wave has passed the bound test: no row maxima from then on
+  bool nomax = false;
+
   const int64_t kend = CAUSAL ? ((q_wg + BM) < p.Sk ? (q_wg + BM) : p.Sk) : p.Sk;
   const int n_kt = static_cast<int>((kend + BN - 1) / BN);   // 64-key sub-tiles
   const int n_st = (n_kt + KT - 1) / KT;                     // LDS stages
@@ -444,6 +494,10 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   };
   // the lazy running max: move mu only when the tile max exceeds it by more than thr, or on the
   // first finite tile (gate is -inf until then); one wave-wide test for all query groups
+  // upper bound on s*c for every key of this lane's query in group n (rescale branch only)
+  auto qbound = [&](const int n) MI355_LAMBDA_INLINE {
+    return qn_lds[n][tid] * kmax * (1.0f + 1.0f / 128) + 1.0f / 128;
+  };
   auto lazy_rescale = [&](f32x16 (&sacc)[QG][2], const float (&mx)[QG]) MI355_LAMBDA_INLINE {
     bool any = false;
 #pragma unroll
@@ -469,11 +523,22 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
         gate[n] = grow ? thr : gate[n];
       }
     }
+    // Key-norm bound test (mu only moves here, so this is the only place it can start to hold):
+    // once every query of the wave has a finite mu and bound - mu <= thr, no later tile max can
+    // exceed the gate, the branch above can never be taken again, and the row maxima that feed
+    // it are skipped from here on -- the results are the same bits.
+    if (use_kb) {
+      bool ok = true;
+#pragma unroll
+      for (int n = 0; n < QG; ++n) ok = ok && gate[n] != NEG_INF && qbound(n) + negmu[n][0] <= thr;
+      if (__builtin_amdgcn_ballot_w64(!ok) == 0) nomax = true;
+    }
   };
   // masks and the lazy running max of sub-tile j; returns after any O/l/mu update
   auto softmax_max = [&](f32x16 (&sacc)[QG][2], const int j, const int st, const int k) MI355_LAMBDA_INLINE {
     uint64_t vbits;
     if (tile_masked(j, st, k, vbits)) mask_scores(sacc, j, vbits);
+    if (nomax) return;
     float mx[QG];
     row_max(sacc, mx);
     lazy_rescale(sacc, mx);
@@ -595,26 +660,31 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
         }
       } else {
         if (j < n_kt && active(j)) {
+          // (nomax: the wave passed the key-norm bound test, no row maxima or rescale test)
           if constexpr (SPLITMAX) {
             // the masking decision first, so that in the common unmasked case the score MFMAs
             // and the row maxima share one basic block and the maxima of the first 32 keys can
-            // issue while the MFMAs of the second 32 run
+            // issue while the MFMAs of the second 32 run (masked sub-tiles, rare, compute the
+            // maxima also under nomax)
             uint64_t vbits;
             float mx[QG];
             if (tile_masked(j, cur, k, vbits)) {
               score(s_a, cur, k);
               mask_scores(s_a, j, vbits);
               row_max(s_a, mx);
+            } else if (nomax) {
+              score(s_a, cur, k);
             } else {
               score(s_a, cur, k);
               row_max(s_a, mx);
             }
-            lazy_rescale(s_a, mx);
+            if (!nomax) lazy_rescale(s_a, mx);
+            exp_pv(s_a, cur, k);
           } else {
             score(s_a, cur, k);
             softmax_max(s_a, j, cur, k);
+            exp_pv(s_a, cur, k);
           }
-          exp_pv(s_a, cur, k);
         }
       }
     }
@@ -696,6 +766,53 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
       }
     }
   }
+}
+
+// Key-norm bounds for the MFMA kernel: out[(b * H + h) * n_chunks + i] = max |k|_2 (fp32) over
+// the keys of chunk i (KB_CHUNK keys) of head (b, h); NaN / inf propagate (the bound test then
+// fails). HD / 8 lanes per key, one 16-byte load each; every lane of a wave runs every pass so the
+// lane-group sums see active partners.
+template <typename T, int HD>
+__global__ __launch_bounds__(256) void attn_key_bound(AttnArgs p, float* __restrict__ out) {
+  constexpr int LK = HD / 8;     // lanes per key
+  constexpr int KPP = 256 / LK;  // keys per pass
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  const T* __restrict__ Kb = static_cast<const T*>(p.k) + b * p.ks0 + h * p.ks2;
+  const int64_t k0 = i * KB_CHUNK;
+  const int64_t nk = (p.Sk - k0) < KB_CHUNK ? (p.Sk - k0) : KB_CHUNK;
+  // UN passes' loads are issued before any is used, so a lane has UN loads in flight
+  constexpr int UN = 8;
+  float m = 0.f;
+  for (int64_t base = 0; base < nk; base += UN * KPP) {
+    u32x4 v[UN];
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const int64_t kk = base + u * KPP + tid / LK;
+      v[u] = u32x4{0u, 0u, 0u, 0u};
+      if (kk < nk) v[u] = *reinterpret_cast<const u32x4*>(Kb + (k0 + kk) * p.ks1 + (tid % LK) * 8);
+    }
+#pragma unroll
+    for (int u = 0; u < UN; ++u) {
+      const typename Mfma<T>::frag f = __builtin_bit_cast(typename Mfma<T>::frag, v[u]);
+      float ss = 0.f;
+#pragma unroll
+      for (int r = 0; r < 8; ++r) {
+        const float x = to_f32(f[r]);
+        ss = __builtin_fmaf(x, x, ss);
+      }
+#pragma unroll
+      for (int off = LK / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+      m = vmax(m, ss);
+    }
+  }
+#pragma unroll
+  for (int off = 32; off >= 1; off >>= 1) m = vmax(m, __shfl_xor(m, off));
+  __shared__ float red[4];
+  if (lane == 0) red[wave] = m;
+  __syncthreads();
+  if (tid == 0)
+    out[(b * p.H + h) * p.kb_n + i] = __builtin_sqrtf(vmax(vmax(red[0], red[1]), vmax(red[2], red[3])));
 }
 
 // VALU kernel: every fp32 problem, and 16-bit head dims the MFMA kernel does not take. LQ lanes
@@ -981,8 +1098,15 @@ void launch_one(const AttnArgs& a, dim3 grid, dim3 block, hipStream_t s) {
 }
 
 template <typename T, int HD, int NW, int QG>
-int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
+int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, float* kb_ws, hipStream_t s) {
   AttnArgs a = a0;
+  if (kb_ws && !(causal && kmask)) {
+    // the key-norm bounds of every head, read by the attention kernel's prologue
+    a.kb_n = static_cast<int>((a.Sk + KB_CHUNK - 1) / KB_CHUNK);
+    hipLaunchKernelGGL((attn_key_bound<T, HD>), dim3(a.kb_n, static_cast<unsigned>(a.H),
+                       static_cast<unsigned>(a.B)), dim3(256), 0, s, a, kb_ws);
+    a.kb = kb_ws;
+  }
   constexpr int BM = NW * 32 * QG;
   a.n_qtiles = static_cast<int>((a.Sq + BM - 1) / BM);
   const dim3 block(NW * 64);
@@ -1066,14 +1190,30 @@ bool head_dim_supported(int64_t hd) {
   }
 }
 
-}  // namespace
+// Key sequences at least this long get the key-norm bound pass from mi355_attn_workspace_bytes.
+// The pass reads K once (per head: S_k rows against the S_q x S_k tiles of the attention), and
+// the row maxima it lets waves skip pay only when a whole work-group's queries pass the bound
+// (small score ranges, as in Q, K ~ N(0,1)/sqrt(head_dim): +5-6% at S = 100000, +14% for
+// head_dim 32); on N(0,1) projections few work-groups pass, so shorter sequences (C3, C4: -1 to
+// -4% with the pass) keep the exact path.
+#ifndef MI355_ATTN_KB_MIN_SK
+#define MI355_ATTN_KB_MIN_SK 32768
+#endif
 
-extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const void* V, void* O,
-                              int64_t B, int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim,
-                              const int64_t* q_strides, const int64_t* k_strides,
-                              const int64_t* v_strides, const int64_t* o_strides, float scale,
-                              int causal, const uint8_t* key_valid, int64_t key_valid_sb,
-                              void* stream) {
+bool on_mfma_kernel(int dtype, int64_t head_dim) {
+  return (dtype == MI355_F16 || dtype == MI355_BF16) &&
+         (head_dim == 32 || head_dim == 64 || head_dim == 128);
+}
+
+int64_t key_bound_bytes(int64_t B, int64_t H, int64_t S_k) {
+  return B * H * ((S_k + KB_CHUNK - 1) / KB_CHUNK) * static_cast<int64_t>(sizeof(float));
+}
+
+int attn_fwd_impl(int dtype, const void* Q, const void* K, const void* V, void* O, int64_t B,
+                  int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim, const int64_t* q_strides,
+                  const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
+                  float scale, int causal, const uint8_t* key_valid, int64_t key_valid_sb,
+                  void* workspace, int64_t workspace_bytes, void* stream) {
   if (B < 0 || H < 0 || S_q < 0 || S_k < 0 || head_dim <= 0) return MI355_E_BAD_SIZE;
   if (B == 0 || H == 0 || S_q == 0) return MI355_OK;
   if (!Q || !K || !V || !O || !q_strides || !k_strides || !v_strides || !o_strides)
@@ -1124,19 +1264,58 @@ extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const voi
   const bool cz = causal != 0;
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (dtype == MI355_F32) return dispatch_valu<float>(a, head_dim, cz, kmask, s);
-  if (head_dim != 32 && head_dim != 64 && head_dim != 128) {
+  if (!on_mfma_kernel(dtype, head_dim)) {
     return dtype == MI355_F16 ? dispatch_valu<_Float16>(a, head_dim, cz, kmask, s)
                               : dispatch_valu<__bf16>(a, head_dim, cz, kmask, s);
   }
+  float* kb = nullptr;
+  if (workspace != nullptr && S_k > 0) {
+    if (workspace_bytes < key_bound_bytes(B, H, S_k)) return MI355_E_BAD_SIZE;
+    if (reinterpret_cast<uintptr_t>(workspace) & 3u) return MI355_E_ALIGNMENT;
+    if ((S_k + KB_CHUNK - 1) / KB_CHUNK > 0x7fffffff) return MI355_E_BAD_SIZE;
+    kb = static_cast<float*>(workspace);
+  }
   if (dtype == MI355_F16) {
     if (head_dim == 32)
-      return launch_mfma<_Float16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, s);
+      return launch_mfma<_Float16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, kb, s);
     return head_dim == 64
-               ? launch_mfma<_Float16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, s)
-               : launch_mfma<_Float16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, s);
+               ? launch_mfma<_Float16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, kb, s)
+               : launch_mfma<_Float16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, kb, s);
   }
-  if (head_dim == 32) return launch_mfma<__bf16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, s);
+  if (head_dim == 32)
+    return launch_mfma<__bf16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, kb, s);
   return head_dim == 64
-             ? launch_mfma<__bf16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, s)
-             : launch_mfma<__bf16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, s);
+             ? launch_mfma<__bf16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, kb, s)
+             : launch_mfma<__bf16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, kb, s);
+}
+
+}  // namespace
+
+extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const void* V, void* O,
+                              int64_t B, int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim,
+                              const int64_t* q_strides, const int64_t* k_strides,
+                              const int64_t* v_strides, const int64_t* o_strides, float scale,
+                              int causal, const uint8_t* key_valid, int64_t key_valid_sb,
+                              void* stream) {
+  return attn_fwd_impl(dtype, Q, K, V, O, B, H, S_q, S_k, head_dim, q_strides, k_strides,
+                       v_strides, o_strides, scale, causal, key_valid, key_valid_sb, nullptr, 0,
+                       stream);
+}
+
+extern "C" int64_t mi355_attn_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t S_q,
+                                              int64_t S_k, int64_t head_dim) {
+  (void)S_q;
+  if (B <= 0 || H <= 0 || S_k < MI355_ATTN_KB_MIN_SK || !on_mfma_kernel(dtype, head_dim)) return 0;
+  return key_bound_bytes(B, H, S_k);
+}
+
+extern "C" int mi355_attn_fwd_ws(int dtype, const void* Q, const void* K, const void* V, void* O,
+                                 int64_t B, int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim,
+                                 const int64_t* q_strides, const int64_t* k_strides,
+                                 const int64_t* v_strides, const int64_t* o_strides, float scale,
+                                 int causal, const uint8_t* key_valid, int64_t key_valid_sb,
+                                 void* workspace, int64_t workspace_bytes, void* stream) {
+  return attn_fwd_impl(dtype, Q, K, V, O, B, H, S_q, S_k, head_dim, q_strides, k_strides,
+                       v_strides, o_strides, scale, causal, key_valid, key_valid_sb, workspace,
+                       workspace_bytes, stream);
 }

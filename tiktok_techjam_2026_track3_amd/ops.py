@@ -206,12 +206,16 @@ def layernorm_linear(x: torch.Tensor, weight: torch.Tensor, colsum: torch.Tensor
 
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[torch.Tensor] = None,
               scale: Optional[float] = None, causal: bool = False,
-              key_valid: Optional[torch.Tensor] = None) -> torch.Tensor:
+              key_valid: Optional[torch.Tensor] = None,
+              key_bound: Optional[bool] = None) -> torch.Tensor:
     """Streamed softmax attention over ``[B, S, H, head_dim]`` views (unit head_dim stride).
 
     ``out`` defaults to a new contiguous ``[B, S_q, H, head_dim]`` tensor, whose
     ``view(B, S_q, H * head_dim)`` is the merged-head context of the reference block.
     ``key_valid`` is an optional ``[B, S_k]`` bool mask of keys to attend to.
+    ``key_bound`` selects the key-norm bound pass of the matrix-core kernel (a workspace of
+    per-chunk max |k| that lets waves skip the per-tile row maxima): None = the library's
+    choice (``mi355_attn_workspace_bytes``: long key ranges), True = always, False = never.
     """
     _on_gpu(q, k, v, out, key_valid)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
@@ -236,14 +240,26 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[t
         kv_ptr = _mask_ptr(key_valid, (B, Sk))
         kv_sb = key_valid.stride(0)
     L = _lib
-    st = L.lib().mi355_attn_fwd(
-        L.dtype_code(dt), q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq, Sk, D,
-        L.i64_array((q.stride(0), q.stride(1), q.stride(2))),
-        L.i64_array((k.stride(0), k.stride(1), k.stride(2))),
-        L.i64_array((v.stride(0), v.stride(1), v.stride(2))),
-        L.i64_array((out.stride(0), out.stride(1), out.stride(2))),
-        float(scale), 1 if causal else 0, kv_ptr, kv_sb, _stream(q))
-    L.check("mi355_attn_fwd", st)
+    code = L.dtype_code(dt)
+    if key_bound is None:
+        ws_bytes = L.lib().mi355_attn_workspace_bytes(code, B, H, Sq, Sk, D)
+    elif key_bound and dt != torch.float32 and D in (32, 64, 128):
+        ws_bytes = B * H * ((Sk + 1023) // 1024) * 4
+    else:
+        ws_bytes = 0
+    args = (code, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq, Sk, D,
+            L.i64_array((q.stride(0), q.stride(1), q.stride(2))),
+            L.i64_array((k.stride(0), k.stride(1), k.stride(2))),
+            L.i64_array((v.stride(0), v.stride(1), v.stride(2))),
+            L.i64_array((out.stride(0), out.stride(1), out.stride(2))),
+            float(scale), 1 if causal else 0, kv_ptr, kv_sb)
+    if ws_bytes > 0:
+        ws = torch.empty((ws_bytes,), device=q.device, dtype=torch.uint8)
+        st = L.lib().mi355_attn_fwd_ws(*args, ws.data_ptr(), ws_bytes, _stream(q))
+        L.check("mi355_attn_fwd_ws", st)
+    else:
+        st = L.lib().mi355_attn_fwd(*args, _stream(q))
+        L.check("mi355_attn_fwd", st)
     return out
 
 
