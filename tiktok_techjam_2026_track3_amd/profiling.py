@@ -35,7 +35,7 @@ import sys
 from collections import defaultdict
 from typing import Dict, List
 
-_OURS = re.compile(r"(gemm_kernel|gemm_splitk|gemm_f32_splitk|attn_fwd_mfma|attn_fwd_valu|attn_fwd_f32|quant_rows_kernel|layernorm_rows|layernorm_stats)(<[^(]*>|I\w*?EEv)?")
+_OURS = re.compile(r"(gemm_kernel|gemm_splitk|gemm_f32_splitk|attn_fwd_mfma|attn_fwd_valu|attn_fwd_f32|attn_key_bound|quant_rows_kernel|layernorm_rows|layernorm_stats)(<[^(]*>|I\w*?EEv)?")
 _MANGLED_ARG = re.compile(r"DF16b|DF16_|Li(-?\d+)E|Lb([01])E|[afhsi]")
 _TYPE = {"DF16b": "bf16", "DF16_": "f16", "a": "i8", "f": "f32", "h": "u8", "s": "i16", "i": "i32"}
 COPY_KERNEL = "neg_kernel"  # the calibration kernel: y = -x, reads and writes every byte once
