@@ -23,7 +23,8 @@
 //   * with key-norm bounds (attn_key_bound: max |k| of the head's keys) a wave whose every
 //     query satisfies |c q| max|k| - mu <= 8 (Cauchy-Schwarz: no later score can exceed the lazy
 //     threshold, so mu can never move again) skips the row maxima and the rescale test for the
-//     rest of its sweep, with bit-identical results.
+//     rest of its sweep, with bit-identical results; non-causal unmasked waves whose bound keeps
+//     every score within +-8 from the start keep mu = 0 (the max-free sweep: branch-free stages).
 // fp32 kernel: one query per lane on VALU (the fp32 configuration is launch-latency bound).
 #include "common.h"
 
@@ -52,10 +53,17 @@ struct AttnArgs {
 
 // Keys per chunk of the key-norm bound pass.
 constexpr int KB_CHUNK = 1024;
+// 1 = waves whose key-norm bound keeps every score within +-8 (log2 units) run the max-free sweep
+#ifndef MI355_ATTN_MAXFREE
+#define MI355_ATTN_MAXFREE 1
+#endif
 
 // MFMA kernel instances that take key-norm bounds
 template <bool PIPE, bool CAUSAL, bool KMASK>
 constexpr bool KB_INSTANCE = !PIPE && !(CAUSAL && KMASK);
+// ... and that run the max-free sweep when the bound allows it (non-causal, no key mask)
+template <bool PIPE, bool CAUSAL, bool KMASK>
+constexpr bool MAXFREE_INSTANCE = !PIPE && !CAUSAL && !KMASK && MI355_ATTN_MAXFREE;
 
 constexpr float NEG_INF = -__builtin_huge_valf();
 
@@ -438,6 +446,24 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
     }
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
   };
+  // S^T of sub-tile j with mu = 0 (the max-free sweep): chains start from zero
+  auto score0 = [&](f32x16 (&sacc)[QG][2], const int st, const int k) MI355_LAMBDA_INLINE {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      frag kf[KS];
+#pragma unroll
+      for (int s = 0; s < KS; ++s) kf[s] = kfrag(st, k, t, s);
+#pragma unroll
+      for (int n = 0; n < QG; ++n) {
+        f32x16 z;
+#pragma unroll
+        for (int i = 0; i < 16; ++i) z[i] = 0.f;
+        sacc[n][t] = MF::mma(kf[0], qf[n][0], z);
+#pragma unroll
+        for (int s = 1; s < KS; ++s) sacc[n][t] = MF::mma(kf[s], qf[n][s], sacc[n][t]);
+      }
+    }
+  };
 
   // masks and the lazy running max of sub-tile j; returns after any O/l/mu update
   // whether sub-tile j needs element masking for this wave (key mask, sequence end, causal
@@ -696,6 +722,36 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   // buffers alternate) so every ring slot and buffer choice is a compile-time constant
   constexpr int U = PIPE ? ((KT % 2 == 0) ? 3 : 6) : NSTAGE;
   int st = 0;
+  if constexpr (MAXFREE_INSTANCE<PIPE, CAUSAL, KMASK>) {
+    // Max-free sweep: when the key-norm bound puts every score of the wave's queries within
+    // [-thr, thr] (|s*c| <= |cq| max|k|), mu stays 0 for the whole sweep: probabilities lie in
+    // [2^-thr, 2^thr] and no row maximum is ever needed. The stages whose sub-tiles are all
+    // full and whose look-ahead loads are all in range run as one branch-free basic block
+    // (score chains from zero, exponentials, P.V), the rest through the generic stage below.
+    bool in_bound = use_kb;
+#pragma unroll
+    for (int n = 0; n < QG; ++n) in_bound = in_bound && qbound(n) <= thr;
+    if (use_kb && __builtin_amdgcn_ballot_w64(!in_bound) == 0) {
+      nomax = true;
+      const int full_st = Sk / (KT * BN);
+      const int load_st = n_kt / KT - NSTAGE + 1;
+      const int n_main = full_st < load_st ? full_st : load_st;
+      auto stage_mf = [&](const int stg, const int cur, const int far) MI355_LAMBDA_INLINE {
+#pragma unroll
+        for (int k = 0; k < KT; ++k) {
+          issue_loads(stg * KT + k + (NSTAGE - 1) * KT, far, k);
+          score0(s_a, cur, k);
+          exp_pv(s_a, cur, k);
+        }
+        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads into slot far have landed
+        __syncthreads();
+      };
+      for (; st + U - 1 < n_main; st += U) {
+#pragma unroll
+        for (int u = 0; u < U; ++u) stage_mf(st + u, u % NSTAGE, (u + NSTAGE - 1) % NSTAGE);
+      }
+    }
+  }
   for (; st + U - 1 < n_st; st += U) {
 #pragma unroll
     for (int u = 0; u < U; ++u)
