@@ -457,3 +457,37 @@ def test_attention_key_bound_nonfinite_and_huge_keys(gpu, bad):
     assert torch.equal(h1a[fin], h1b[fin])
     assert torch.isfinite(b[:, :, 0]).all()
     assert float((a[:, :, 0].float() - b[:, :, 0].float()).abs().max()) < 1e-3
+
+
+# ------------------------------------------------------------ all-true key mask (device check)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hd", [32, 64, 128])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("S", [1, 17, 130, 1000, 2053])
+def test_attention_all_true_mask_same_bits(gpu, dtype, hd, causal, S):
+    """A key mask that is all true over a work-group's keys is recognised on the device (one
+    scan of the row's bytes), after which the sweep runs as without a mask: the same bits as
+    the call without a mask, for row lengths that leave misaligned heads and byte tails."""
+    ops = _ops()
+    print(f"all-true mask dtype={dtype} hd={hd} causal={causal} S={S}", flush=True)
+    B, H = 2, 2
+    q = _rand((B, S, H, hd), dtype, 81).to(gpu)
+    k = _rand((B, S, H, hd), dtype, 82).to(gpu)
+    v = _rand((B, S, H, hd), dtype, 83).to(gpu)
+    mask = torch.ones(B, S, dtype=torch.bool, device=gpu)
+    a = ops.attention(q, k, v, causal=causal, key_valid=mask)
+    b = ops.attention(q, k, v, causal=causal)
+    assert torch.equal(a, b)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("pos", [0, 5, 16, 1024, 2040, 2052])
+def test_attention_single_invalid_key_is_seen(gpu, dtype, causal, pos):
+    """One invalid key anywhere in a row (the misaligned head, the 16-byte body, the byte tail;
+    row stride 2053 bytes, so the second row starts misaligned) must switch that work-group back
+    to the masked sweep: checked against the oracle; the other row is all true."""
+    B, S = 2, 2053
+    mask = torch.ones(B, S, dtype=torch.bool)
+    mask[1, pos] = False   # (causal, pos 0: query 0 of row 1 has no valid key, NaN as in the oracle)
+    _attn_check(gpu, dtype, B, 2, S, S, 64, causal, key_valid=mask, seed=91)
