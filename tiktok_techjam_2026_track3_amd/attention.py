@@ -40,6 +40,7 @@ import torch
 import torch.nn as nn
 
 from . import ops
+from .graph import AutoGraph, version_of
 
 _CACHE_KEYS = ("_mi355_pack", "_mi355_lnpack")
 
@@ -49,7 +50,7 @@ MFMA_HEAD_DIMS = (32, 64, 128)
 
 def norm_stamp(norm: nn.Module) -> Tuple:
     """Identity of a LayerNorm's parameters (storage, version, dtype, device) and eps."""
-    return tuple((p.data_ptr(), p._version, p.dtype, p.device) if p is not None else None
+    return tuple((p.data_ptr(), version_of(p), p.dtype, p.device) if p is not None else None
                  for p in (norm.weight, norm.bias)) + (float(norm.eps),)
 
 
@@ -108,7 +109,7 @@ class SelfAttention(nn.Module):
         stamp = []
         for lin in (self.q_proj, self.k_proj, self.v_proj, self.out_proj):
             for p in (lin.weight, lin.bias):
-                stamp.append((p.data_ptr(), p._version, p.dtype, p.device))
+                stamp.append((p.data_ptr(), version_of(p), p.dtype, p.device))
         return tuple(stamp)
 
     def _cached(self, key, build):
@@ -190,8 +191,19 @@ class SelfAttention(nn.Module):
         qkv5 = qkv.view(B, S, 3, self.num_heads, self.head_dim)
         return qkv5[:, :, 0], qkv5[:, :, 1], qkv5[:, :, 2]
 
+    # launch-bound forwards (small inputs, inference) replay a captured graph (graph.AutoGraph)
+    auto_graph = True
+
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,
                 causal: bool = False) -> torch.Tensor:
+        if self.auto_graph:
+            ag = self.__dict__.get("_autograph")
+            if ag is None:
+                ag = self.__dict__["_autograph"] = AutoGraph()
+            out = ag(self, lambda sx, sm: self.run(sx, sm, causal), x, valid_token_mask,
+                     (bool(causal),))
+            if out is not None:
+                return out
         return self.run(x, valid_token_mask, causal)
 
     def run(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,

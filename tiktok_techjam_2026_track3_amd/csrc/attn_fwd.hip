@@ -797,7 +797,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   // Needs 16-byte aligned output rows; otherwise the runs are stored directly.
   constexpr int OPITCH = HD * 2 + 16;  // padded row pitch of the staged tile (bank spread)
   constexpr int OCH = HD * 2 / 16;     // 16-byte chunks per output row
-  static_assert(NW % 2 == 0 && (NW / 2) * QW * OPITCH <= static_cast<int>(sizeof(k_lds)),
+  static_assert(!MI355_ATTN_OSTAGE || (NW % 2 == 0 && (NW / 2) * QW * OPITCH <= static_cast<int>(sizeof(k_lds))),
                 "output staging fits the K (and V) ring");
   // (fp16 instances: the bf16 head_dim-64 key-masked instance, whose fp32 row sums already hold
   // it at the register limit, would spill)

@@ -21,10 +21,19 @@ the module had then, and keeps them alive): calling it with other inputs, after 
 """
 from __future__ import annotations
 
+import weakref
+from collections import OrderedDict
 from typing import Optional
 
 import torch
 import torch.nn as nn
+
+
+def version_of(t: torch.Tensor) -> int:
+    """The tensor's in-place version counter; -1 for inference tensors, which keep none (their
+    in-place updates under torch.inference_mode cannot be seen: caches keyed on them rely on
+    load_state_dict / _apply invalidating explicitly)."""
+    return -1 if t.is_inference() else t._version
 
 
 class GraphedForward:
@@ -66,7 +75,7 @@ class GraphedForward:
 
     def _params_stamp(self):
         mods = [self.module] + ([self.norm] if self.norm is not None else [])
-        return tuple((p.data_ptr(), p._version) for m in mods for p in m.parameters())
+        return tuple((p.data_ptr(), version_of(p)) for m in mods for p in m.parameters())
 
     def _run(self) -> torch.Tensor:
         if self.norm is not None:
@@ -89,3 +98,157 @@ class GraphedForward:
                 self.static_mask.copy_(valid_token_mask)
             self.graph.replay()
             return self.static_out.clone()
+
+
+# Input elements at or below which a module's forward replays a captured graph (AutoGraph): an
+# attention block of 128 x 256 (the fp32 configuration) spends ~18 us on the GPU against ~70 us
+# of host work per eager forward; at 2^20 elements the kernels' time already exceeds the host's.
+AUTO_GRAPH_MAX_ELEMS = 1 << 20
+
+
+# Parameter or submodule registrations anywhere in the process (construction, replacement by
+# assignment) bump this epoch, so a capture can tell in O(1) that the module it read may have
+# other parameter objects now; in-place updates, load_state_dict and _apply are seen through the
+# parameters' version counters, data pointers and the derived-weight caches.
+_REGISTRATION_EPOCH = [0]
+
+
+def _bump_epoch(*_args) -> None:
+    _REGISTRATION_EPOCH[0] += 1
+
+
+_REGISTRATION_HOOKS = (
+    torch.nn.modules.module.register_module_parameter_registration_hook(_bump_epoch),
+    torch.nn.modules.module.register_module_module_registration_hook(_bump_epoch),
+)
+
+
+def _derived_caches(module: nn.Module):
+    """(submodule, attribute, object) of every derived-weight cache the forward reads by address
+    (module attributes named _mi355_*: packed, LayerNorm-folded and quantised weights)."""
+    return [(m, k, v) for m in module.modules() for k, v in m.__dict__.items()
+            if k.startswith("_mi355_")]
+
+
+class _Capture:
+    """One captured forward: static input buffers, the graph, its output, and what it read."""
+
+    def __init__(self, module: nn.Module, fn, x: torch.Tensor, mask: Optional[torch.Tensor]):
+        self.static_x = x.detach().clone()
+        self.static_mask = None if mask is None else mask.detach().clone()
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            for _ in range(2):
+                fn(self.static_x, self.static_mask)
+        torch.cuda.current_stream().wait_stream(side)
+        self.graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(self.graph):
+            self.static_out = fn(self.static_x, self.static_mask)
+        self.epoch = _REGISTRATION_EPOCH[0]
+        self.cls = type(module)
+        self.params = list(module.parameters())
+        self.tracked = [p for p in self.params if not p.is_inference()]
+        self.ptrs = [p.data_ptr() for p in self.params]
+        self.vers = [p._version for p in self.tracked]
+        self.caches = _derived_caches(module)   # held: keeps what the graph reads alive
+        self.last = (None, None)                # (weak reference, version) of the inputs copied
+
+    def current(self, module: nn.Module) -> bool:
+        """The module still has the parameters, values and derived weights the graph read (the
+        parameter list is walked only when a registration happened somewhere: that walk costs
+        ~7 us for an attention block, ~70 us for a 4-layer model, per call)."""
+        if type(module) is not self.cls:
+            return False
+        if _REGISTRATION_EPOCH[0] != self.epoch:
+            now = list(module.parameters())
+            if len(now) != len(self.params) or any(a is not b for a, b in zip(now, self.params)):
+                return False
+            self.epoch = _REGISTRATION_EPOCH[0]
+        return ([p._version for p in self.tracked] == self.vers
+                and [p.data_ptr() for p in self.params] == self.ptrs
+                and all(m.__dict__.get(k) is v for m, k, v in self.caches))
+
+    def replay(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
+        # The copy is skipped when the caller hands back the same tensor objects with unchanged
+        # version counters (the benchmark's timing loop passes one x throughout); any in-place
+        # torch update of x or the mask (or of a view of them) bumps the counter. Inference
+        # tensors keep no version counter, so they are always copied.
+        ref, ver = self.last
+        tracked = not x.is_inference() and (mask is None or not mask.is_inference())
+        key = (x._version, None if mask is None else mask._version) if tracked else None
+        same = (tracked and ref is not None and ref[0]() is x
+                and (mask is None) == (ref[1] is None)
+                and (mask is None or ref[1]() is mask) and ver == key)
+        if not same:
+            self.static_x.copy_(x)
+            if mask is not None:
+                self.static_mask.copy_(mask)
+            self.last = ((weakref.ref(x), None if mask is None else weakref.ref(mask)), key)
+        self.graph.replay()
+        return self.static_out.clone()
+
+
+class AutoGraph:
+    """Graph replay inside a module's forward for launch-bound calls (the reference's route:
+    the first forward eager, the second captured, later ones replayed,
+    Project/submission/dispatcher_region.py:1220-1363).
+
+    ``__call__(module, fn, x, mask, extra)`` returns ``fn(x, mask)``'s result from a replay, or
+    None when the caller should run eagerly: a CPU or large input (more than
+    AUTO_GRAPH_MAX_ELEMS elements), autograd enabled, a capture already in progress (the caller's
+    own graph then records the eager kernels), the first call of an input signature, or a
+    capture that no longer matches the module (its parameters or derived weights changed: the
+    graph is dropped and the next call captures again). The signature is x's and the mask's
+    shape, dtype, device and strides plus ``extra`` (e.g. the causal flag); up to ``max_graphs``
+    signatures keep their graphs. Outputs are fresh tensors (a clone of the graph's output)."""
+
+    def __init__(self, max_graphs: int = 4):
+        self.max_graphs = max_graphs
+        self.entries: "OrderedDict[tuple, dict]" = OrderedDict()
+
+    # copies of a module (deepcopy, pickling) start without captures: a graph belongs to the
+    # module and buffers it was recorded with
+    def __deepcopy__(self, memo):
+        return AutoGraph(self.max_graphs)
+
+    def __getstate__(self):
+        return {"max_graphs": self.max_graphs}
+
+    def __setstate__(self, state):
+        self.__init__(state["max_graphs"])
+
+    @staticmethod
+    def applies(x: torch.Tensor) -> bool:
+        return (x.is_cuda and x.numel() <= AUTO_GRAPH_MAX_ELEMS and not torch.is_grad_enabled()
+                and not torch.cuda.is_current_stream_capturing())
+
+    def __call__(self, module: nn.Module, fn, x: torch.Tensor, mask: Optional[torch.Tensor],
+                 extra=()) -> Optional[torch.Tensor]:
+        if not self.applies(x) or (mask is not None and not mask.is_cuda):
+            return None
+        key = (tuple(x.shape), x.dtype, x.device, tuple(x.stride()),
+               None if mask is None else (tuple(mask.shape), mask.dtype, tuple(mask.stride())),
+               extra)
+        e = self.entries.get(key)
+        if e is None:
+            e = self.entries[key] = {"calls": 0, "cap": None, "failed": False}
+            while len(self.entries) > self.max_graphs:
+                self.entries.popitem(last=False)
+        else:
+            self.entries.move_to_end(key)
+        if e["failed"]:
+            return None
+        cap = e["cap"]
+        if cap is not None and not cap.current(module):
+            e["cap"], e["calls"], cap = None, 0, None
+        if cap is None:
+            e["calls"] += 1
+            if e["calls"] < 2:
+                return None
+            try:
+                cap = e["cap"] = _Capture(module, fn, x, mask)
+            except RuntimeError:
+                e["failed"] = True   # not capturable here: this signature stays eager
+                return None
+        return cap.replay(x, mask)

@@ -36,10 +36,11 @@ import torch.nn as nn
 
 from . import ops
 from .attention import Int8SelfAttention, SelfAttention
+from .graph import AutoGraph, version_of
 
 
 def _stamp(*params):
-    return tuple((p.data_ptr(), p._version, p.dtype, p.device) for p in params if p is not None)
+    return tuple((p.data_ptr(), version_of(p), p.dtype, p.device) for p in params if p is not None)
 
 
 def _ffn_weights(block: nn.Module, dtype: torch.dtype, device: torch.device):
@@ -258,7 +259,22 @@ class Transformer(nn.Module):
              for _ in range(config.num_layers)])
         self.final_norm = nn.LayerNorm(config.d_model)
 
+    # launch-bound forwards (small inputs, inference) replay a captured graph (graph.AutoGraph),
+    # as the reference's optimised model does (Project/submission/dispatcher_region.py:1220-1363)
+    auto_graph = True
+
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
+        if self.auto_graph:
+            ag = self.__dict__.get("_autograph")
+            if ag is None:
+                ag = self.__dict__["_autograph"] = AutoGraph()
+            out = ag(self, self._eager_forward, x, valid_token_mask, (bool(self.config.causal),))
+            if out is not None:
+                return out
+        return self._eager_forward(x, valid_token_mask)
+
+    def _eager_forward(self, x: torch.Tensor,
+                       valid_token_mask: Optional[torch.Tensor] = None) -> torch.Tensor:
         for layer in self.layers:
             x = layer(x, valid_token_mask, self.config.causal)
         return final_norm_forward(self.final_norm, x, valid_token_mask)
