@@ -179,6 +179,18 @@ int mi355_layernorm(int dtype, const void* X, int64_t ldx, const void* gamma, co
                     float eps, void* Y, int64_t ldy, int64_t M, int64_t K, void* stream);
 
 /*
+ * nn.LayerNorm as mi355_layernorm, with the normalised rows written in another type:
+ * out_dtype == dtype is mi355_layernorm; dtype F32 with out_dtype F16 computes in fp32 and rounds
+ * the result once to fp16 (the fp16 operand of an fp32 model's projection: the reference's fast
+ * route runs fp32 models on fp16 tiles, Project/submission/dispatcher_region.py:1017-1091, with
+ * the LayerNorm fused into its QKV kernel, :343-399). Other pairs: MI355_E_UNSUPPORTED.
+ * F32 -> F16: K, ldx, ldy multiples of 4, X 16-byte and Y 8-byte aligned.
+ */
+int mi355_layernorm_cvt(int dtype, int out_dtype, const void* X, int64_t ldx, const void* gamma,
+                        const void* beta, float eps, void* Y, int64_t ldy, int64_t M, int64_t K,
+                        void* stream);
+
+/*
  * Projection with the block's residual add fused into its epilogue:
  *   C = R + out_dtype(A · W^T + bias)
  * i.e. `x + self.attention(...)` of BaselineTransformerBlock.forward

@@ -163,6 +163,12 @@ def test_attention_half_is_the_unfused_composition(gpu, name, masked):
     w, params, x, norm, _, valid, mod = _half_case(name, 1234, gpu, masked)
     xg = x.to(gpu)
     vg = None if valid is None else valid.to(gpu)
+    if w.dtype == torch.float32:
+        # the fp32-operand path, whose unfused form is this composition; the default fp16
+        # operands of an fp32 model are judged against it below
+        with torch.inference_mode():
+            fp16_ops = mod.forward_residual(xg, norm, vg, w.causal)
+        mod.fp32_operand_dtype = torch.float32
     with torch.inference_mode():
         mod.fold_norm = False
         fused = mod.forward_residual(xg, norm, vg, w.causal)
@@ -182,6 +188,12 @@ def test_attention_half_is_the_unfused_composition(gpu, name, masked):
     if valid is not None:
         assert torch.equal(fused[~vg], xg[~vg])
         assert torch.equal(folded[~vg], xg[~vg])
+    if w.dtype == torch.float32:
+        r = compare_outputs(comp.cpu(), fp16_ops.cpu())
+        print(f"fp16-operand half {name} vs the fp32-operand composition: {r.summary()}", flush=True)
+        assert r.passed, r.summary()
+        if valid is not None:
+            assert torch.equal(fp16_ops[~vg], xg[~vg])
 
 
 # ------------------------------------------------- LayerNorm folded into the projection GEMM

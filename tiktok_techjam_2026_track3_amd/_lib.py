@@ -43,6 +43,9 @@ _SIGNATURES = {
     ),
     "mi355_quant_rows_i8": (C.c_int, [C.c_int, _P, _I64, _P, _P, _I64, _I64, C.c_int, _P]),
     "mi355_layernorm": (C.c_int, [C.c_int, _P, _I64, _P, _P, C.c_float, _P, _I64, _I64, _I64, _P]),
+    "mi355_layernorm_cvt": (
+        C.c_int, [C.c_int, C.c_int, _P, _I64, _P, _P, C.c_float, _P, _I64, _I64, _I64, _P],
+    ),
     "mi355_gemm_bias_residual": (
         C.c_int,
         [C.c_int, C.c_int, _P, _I64, _P, _I64, _P, _P, _I64, _P, _I64, _I64, _I64, _I64, _P, _P],

@@ -70,12 +70,29 @@ class SelfAttention(nn.Module):
     # plain projection instead
     fold_norm = True
 
+    # fp32 models whose core is fp16 (the matrix-core head dims): the block's projections take
+    # fp16 operands too -- the LayerNorms compute in fp32 and write fp16, the weights are packed
+    # in fp16, accumulation and the residual stream stay fp32 -- as the reference's fast route
+    # runs fp32 models on fp16 tiles (Project/submission/dispatcher_region.py:1017-1091);
+    # torch.float32 keeps fp32 operands (the LayerNorms then folded into the projections)
+    fp32_operand_dtype = torch.float16
+
+    def operand_dtype(self, dtype: torch.dtype) -> torch.dtype:
+        """Operand dtype of the block's projections (forward_residual, the FFN half) for model
+        dtype ``dtype``."""
+        if dtype == torch.float32 and self.core_dtype(dtype) == torch.float16:
+            return self.fp32_operand_dtype
+        return dtype
+
     def folds_norm(self, dtype: torch.dtype) -> bool:
         """Whether forward_residual (and the block's FFN half) fold the LayerNorm for inputs of
         ``dtype``. bf16 keeps the LayerNorm kernel: the fold rounds gamma * W to bf16 where the
         reference rounds the normalised activations, and at bf16's 8-bit precision that moves
-        about one output in 10^4 by a bf16 step beyond the reference's own rounding points."""
-        return bool(self.fold_norm) and dtype != torch.bfloat16
+        about one output in 10^4 by a bf16 step beyond the reference's own rounding points.
+        fp32 models on fp16 operands also run the LayerNorm kernel (fp32 statistics, fp16
+        output): folding would round the raw x to fp16, whose mean need not be small."""
+        return (bool(self.fold_norm) and dtype != torch.bfloat16
+                and self.operand_dtype(dtype) == dtype)
 
     def __init__(self, d_model: int, num_heads: int) -> None:
         super().__init__()
@@ -264,7 +281,8 @@ class SelfAttention(nn.Module):
             if t is not None and (t.dtype != x.dtype or t.device != x.device):
                 raise ValueError("norm parameters must be on x's device in x's dtype")
         key_valid, row_valid = self._resolve_mask(valid_token_mask, B, S, x.device)
-        w_qkv, b_qkv, w_o, b_o = self._packed_weights(x.dtype, x.device)
+        op = self.operand_dtype(x.dtype)
+        w_qkv, b_qkv, w_o, b_o = self._packed_weights(op, x.device)
         core = self.core_dtype(x.dtype)
         x2 = x.reshape(B * S, d)
         if not x2.is_contiguous():
@@ -276,7 +294,7 @@ class SelfAttention(nn.Module):
         else:
             mark("norm")
             h = ops.layer_norm(x2, w_n.detach() if w_n is not None else None,
-                               b_n.detach() if b_n is not None else None, norm.eps)
+                               b_n.detach() if b_n is not None else None, norm.eps, out_dtype=op)
             mark("qkv")
             qkv = ops.linear(h, w_qkv, b_qkv, out_dtype=core)
         q, k, v = self._qkv_views(qkv, B, S)

@@ -13,22 +13,25 @@ MI355_DEVINL float wave_sum(float v) {
   return v;
 }
 
-template <typename T, int NV>
+// TO: output type (the input type, or fp16 for an fp32 input: the fp16 operands of an fp32
+// model's projections)
+template <typename T, int NV, typename TO = T>
 __global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, int64_t ldx,
                                                       const T* __restrict__ gamma,
                                                       const T* __restrict__ beta, float eps,
-                                                      T* __restrict__ Y, int64_t ldy, int64_t M,
+                                                      TO* __restrict__ Y, int64_t ldy, int64_t M,
                                                       int K, const uint8_t* __restrict__ row_valid) {
   constexpr int EPV = 16 / static_cast<int>(sizeof(T));  // elements per 16-byte vector
   typedef T tv __attribute__((ext_vector_type(EPV)));
+  typedef TO tov __attribute__((ext_vector_type(EPV)));
   const int lane = threadIdx.x & 63;
   const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
   if (row >= M) return;  // whole wave leaves together
   const int nvec = K / EPV;
   if (row_valid != nullptr && row_valid[row] == 0) {
     // masked row: zeros (the masked_fill that follows the final norm)
-    T* yr = Y + row * ldy;
-    for (int vi = lane; vi < nvec; vi += 64) *reinterpret_cast<tv*>(yr + static_cast<int64_t>(vi) * EPV) = tv{};
+    TO* yr = Y + row * ldy;
+    for (int vi = lane; vi < nvec; vi += 64) *reinterpret_cast<tov*>(yr + static_cast<int64_t>(vi) * EPV) = tov{};
     return;
   }
   const T* xr = X + row * ldx;
@@ -61,7 +64,7 @@ __global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, i
   const float var = wave_sum(sq) / static_cast<float>(K);
   const float rstd = 1.0f / sqrtf(var + eps);
 
-  T* yr = Y + row * ldy;
+  TO* yr = Y + row * ldy;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
     const int vi = lane + 64 * j;
@@ -69,15 +72,15 @@ __global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, i
     tv gv, bv;
     if (gamma) gv = *reinterpret_cast<const tv*>(gamma + static_cast<int64_t>(vi) * EPV);
     if (beta) bv = *reinterpret_cast<const tv*>(beta + static_cast<int64_t>(vi) * EPV);
-    tv out;
+    tov out;
 #pragma unroll
     for (int e = 0; e < EPV; ++e) {
       float y = (xs[j][e] - mean) * rstd;
       if (gamma) y = y * to_f32(gv[e]);
       if (beta) y = y + to_f32(bv[e]);
-      out[e] = from_f32<T>(y);
+      out[e] = from_f32<TO>(y);
     }
-    *reinterpret_cast<tv*>(yr + static_cast<int64_t>(vi) * EPV) = out;
+    *reinterpret_cast<tov*>(yr + static_cast<int64_t>(vi) * EPV) = out;
   }
 }
 
@@ -152,7 +155,7 @@ int launch_stats(const void* X, int64_t ldx, float eps, float* stats, int64_t M,
   return static_cast<int>(hipGetLastError());
 }
 
-template <typename T>
+template <typename T, typename TO = T>
 int launch_ln(const void* X, int64_t ldx, const void* gamma, const void* beta, float eps, void* Y,
               int64_t ldy, int64_t M, int64_t K, const uint8_t* rv, hipStream_t s) {
   constexpr int EPV = 16 / static_cast<int>(sizeof(T));
@@ -163,18 +166,18 @@ int launch_ln(const void* X, int64_t ldx, const void* gamma, const void* beta, f
   const T* x = static_cast<const T*>(X);
   const T* g = static_cast<const T*>(gamma);
   const T* b = static_cast<const T*>(beta);
-  T* y = static_cast<T*>(Y);
+  TO* y = static_cast<TO*>(Y);
   const int k = static_cast<int>(K);
   if (nvec <= 64)
-    hipLaunchKernelGGL((layernorm_rows<T, 1>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+    hipLaunchKernelGGL((layernorm_rows<T, 1, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   else if (nvec <= 128)
-    hipLaunchKernelGGL((layernorm_rows<T, 2>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+    hipLaunchKernelGGL((layernorm_rows<T, 2, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   else if (nvec <= 256)
-    hipLaunchKernelGGL((layernorm_rows<T, 4>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+    hipLaunchKernelGGL((layernorm_rows<T, 4, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   else if (nvec <= 512)
-    hipLaunchKernelGGL((layernorm_rows<T, 8>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+    hipLaunchKernelGGL((layernorm_rows<T, 8, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   else
-    hipLaunchKernelGGL((layernorm_rows<T, 16>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+    hipLaunchKernelGGL((layernorm_rows<T, 16, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -217,4 +220,29 @@ extern "C" int mi355_layernorm(int dtype, const void* X, int64_t ldx, const void
                                const void* beta, float eps, void* Y, int64_t ldy, int64_t M,
                                int64_t K, void* stream) {
   return mi355_layernorm_masked(dtype, X, ldx, gamma, beta, eps, Y, ldy, M, K, nullptr, stream);
+}
+
+extern "C" int mi355_layernorm_cvt(int dtype, int out_dtype, const void* X, int64_t ldx,
+                                   const void* gamma, const void* beta, float eps, void* Y,
+                                   int64_t ldy, int64_t M, int64_t K, void* stream) {
+  if (out_dtype == dtype)
+    return mi355_layernorm_masked(dtype, X, ldx, gamma, beta, eps, Y, ldy, M, K, nullptr, stream);
+  if (dtype != MI355_F32 || out_dtype != MI355_F16) {
+    if ((dtype != MI355_F32 && dtype != MI355_F16 && dtype != MI355_BF16) ||
+        (out_dtype != MI355_F32 && out_dtype != MI355_F16 && out_dtype != MI355_BF16))
+      return MI355_E_BAD_DTYPE;
+    return MI355_E_UNSUPPORTED;
+  }
+  if (M < 0 || K <= 0) return MI355_E_BAD_SIZE;
+  if (M == 0) return MI355_OK;
+  if (!X || !Y) return MI355_E_NULL_POINTER;
+  if (!(eps >= 0.f)) return MI355_E_BAD_SIZE;
+  // fp32 rows read as 16-byte vectors of 4, fp16 rows written as 8-byte vectors of 4
+  if (K % 4 || ldx % 4 || ldy % 4 || !aligned16(X) || (reinterpret_cast<uintptr_t>(Y) & 7u) ||
+      (gamma && !aligned16(gamma)) || (beta && !aligned16(beta)))
+    return MI355_E_ALIGNMENT;
+  if (ldx < K || ldy < K) return MI355_E_BAD_SIZE;
+  if (K / 4 > 64 * 16) return MI355_E_UNSUPPORTED;  // row must fit the registers of one wave
+  return launch_ln<float, _Float16>(X, ldx, gamma, beta, eps, Y, ldy, M, K, nullptr,
+                                    static_cast<hipStream_t>(stream));
 }

@@ -111,9 +111,11 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
 
 def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[torch.Tensor],
                eps: float = 1e-5, out: Optional[torch.Tensor] = None,
-               row_valid: Optional[torch.Tensor] = None) -> torch.Tensor:
+               row_valid: Optional[torch.Tensor] = None,
+               out_dtype: Optional[torch.dtype] = None) -> torch.Tensor:
     """Row LayerNorm of a 2-D ``x`` (nn.LayerNorm over the last dimension): fp32 statistics,
-    output rounded once to x's dtype. ``weight``/``bias`` are contiguous ``[K]`` of x's dtype.
+    output rounded once to x's dtype, or to ``out_dtype`` (fp16 for an fp32 x: the fp16 operand
+    of an fp32 model's projection). ``weight``/``bias`` are contiguous ``[K]`` of x's dtype.
     Rows whose ``row_valid`` entry is False are written as zeros."""
     _on_gpu(x, weight, bias, out, row_valid)
     if x.dim() != 2 or x.stride(1) != 1:
@@ -122,10 +124,21 @@ def layer_norm(x: torch.Tensor, weight: Optional[torch.Tensor], bias: Optional[t
     for t in (weight, bias):
         if t is not None and (t.shape != (K,) or t.dtype != x.dtype or not t.is_contiguous()):
             raise ValueError(f"LayerNorm weight/bias must be contiguous [{K}] of x's dtype")
+    odt = out_dtype or (out.dtype if out is not None else x.dtype)
     if out is None:
-        out = torch.empty((M, K), device=x.device, dtype=x.dtype)
-    elif out.shape != (M, K) or out.dtype != x.dtype or out.stride(1) != 1:
-        raise ValueError("out must be [M, K] of x's dtype with unit column stride")
+        out = torch.empty((M, K), device=x.device, dtype=odt)
+    elif out.shape != (M, K) or out.dtype != odt or out.stride(1) != 1:
+        raise ValueError("out must be [M, K] of the output dtype with unit column stride")
+    if odt != x.dtype:
+        if row_valid is not None:
+            raise ValueError("a converting LayerNorm takes no row mask")
+        st = _lib.lib().mi355_layernorm_cvt(
+            _lib.dtype_code(x.dtype), _lib.dtype_code(odt), x.data_ptr(), x.stride(0),
+            weight.data_ptr() if weight is not None else 0,
+            bias.data_ptr() if bias is not None else 0, float(eps), out.data_ptr(), out.stride(0),
+            M, K, _stream(x))
+        _lib.check("mi355_layernorm_cvt", st)
+        return out
     if row_valid is not None:
         st = _lib.lib().mi355_layernorm_masked(
             _lib.dtype_code(x.dtype), x.data_ptr(), x.stride(0),

@@ -146,16 +146,19 @@ def block_forward(block: nn.Module, x: torch.Tensor, valid_token_mask: Optional[
     x1 = attn.forward_residual(x, block.norm1, valid_token_mask, causal, marks=inner)
     x1 = x1.reshape(B * S, d)
     w2, b2 = _norm_params(block.norm2, x)
-    w_in, b_in, w_out, b_out = _ffn_weights(block, x.dtype, x.device)
+    # the FFN's operand dtype: the model's, or fp16 for fp32 models with an fp16 attention core
+    # (SelfAttention.operand_dtype; the GELU output is then fp16 too, the residual stream fp32)
+    op = attn.operand_dtype(x.dtype)
+    w_in, b_in, w_out, b_out = _ffn_weights(block, op, x.device)
     if attn.folds_norm(x.dtype):
         wf, colsum, bf = _ffn_in_folded(block, x.dtype, x.device)
         mark("ffn_in")
         g = ops.layernorm_linear(x1, wf, colsum, bf, block.norm2.eps, gelu=True)
     else:
         mark("norm2")
-        h2 = ops.layer_norm(x1, w2, b2, block.norm2.eps)
+        h2 = ops.layer_norm(x1, w2, b2, block.norm2.eps, out_dtype=op)
         mark("ffn_in")
-        g = ops.linear(h2, w_in, b_in, gelu=True, out_dtype=x.dtype)
+        g = ops.linear(h2, w_in, b_in, gelu=True, out_dtype=op)
     mark("ffn_out")
     y = ops.linear(g, w_out, b_out, residual=x1, row_valid=row_valid, zero_masked_rows=True,
                    out_dtype=x.dtype)
