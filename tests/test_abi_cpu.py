@@ -211,3 +211,23 @@ def test_build_refuses_lds_dma_kernels_that_use_scratch():
         B.check_no_scratch("a.hip", usage)
     # the vector-ALU kernel issues no LDS-DMA loads: not checked
     B.check_no_scratch("a.hip", {k: v for k, v in usage.items() if "valu" in k})
+
+
+def test_layernorm_cvt_argument_validation():
+    """mi355_layernorm_cvt: same-dtype calls are mi355_layernorm; fp32 -> fp16 is the one
+    converting pair; the checks run before any launch."""
+    L = _lib()
+    h = L.lib()
+    codes = _status_codes()
+    fake = 1 << 20
+    cvt = h.mi355_layernorm_cvt
+    assert cvt(0, 2, fake, 64, None, None, 1e-5, fake, 64, 4, 64, None) == codes["MI355_E_UNSUPPORTED"]
+    assert cvt(1, 0, fake, 64, None, None, 1e-5, fake, 64, 4, 64, None) == codes["MI355_E_UNSUPPORTED"]
+    assert cvt(0, 7, fake, 64, None, None, 1e-5, fake, 64, 4, 64, None) == codes["MI355_E_BAD_DTYPE"]
+    assert cvt(0, 1, fake, 64, None, None, 1e-5, fake, 64, 4, 62, None) == codes["MI355_E_ALIGNMENT"]
+    assert cvt(0, 1, fake, 64, None, None, 1e-5, fake + 4, 64, 4, 64, None) == codes["MI355_E_ALIGNMENT"]
+    assert cvt(0, 1, None, 64, None, None, 1e-5, fake, 64, 4, 64, None) == codes["MI355_E_NULL_POINTER"]
+    assert cvt(0, 1, fake, 64, None, None, -1.0, fake, 64, 4, 64, None) == codes["MI355_E_BAD_SIZE"]
+    assert cvt(0, 1, fake, 32, None, None, 1e-5, fake, 64, 4, 64, None) == codes["MI355_E_BAD_SIZE"]
+    assert cvt(0, 1, fake, 8192, None, None, 1e-5, fake, 8192, 4, 8192, None) == codes["MI355_E_UNSUPPORTED"]
+    assert cvt(0, 1, fake, 64, None, None, 1e-5, fake, 64, 0, 64, None) == 0

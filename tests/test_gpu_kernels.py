@@ -491,3 +491,20 @@ def test_attention_single_invalid_key_is_seen(gpu, dtype, causal, pos):
     mask = torch.ones(B, S, dtype=torch.bool)
     mask[1, pos] = False   # (causal, pos 0: query 0 of row 1 has no valid key, NaN as in the oracle)
     _attn_check(gpu, dtype, B, 2, S, S, 64, causal, key_valid=mask, seed=91)
+
+
+@pytest.mark.parametrize("K", [64, 1024, 4096])
+def test_layer_norm_fp32_to_fp16_is_the_rounded_fp32_result(gpu, K):
+    """mi355_layernorm_cvt fp32 -> fp16: the same fp32 computation as the fp32 LayerNorm kernel,
+    rounded once to fp16 (round to nearest even, as torch's .half())."""
+    ops = _ops()
+    M = 300
+    x = _rand((M, K), torch.float32, 101, scale=3.0)
+    x[5] += 100.0                                  # a row with a large mean
+    w = _rand((K,), torch.float32, 102)
+    b = _rand((K,), torch.float32, 103)
+    xg, wg, bg = x.to(gpu), w.to(gpu), b.to(gpu)
+    y32 = ops.layer_norm(xg, wg, bg, 1e-5)
+    y16 = ops.layer_norm(xg, wg, bg, 1e-5, out_dtype=torch.float16)
+    assert y16.dtype == torch.float16
+    assert torch.equal(y16, y32.half())
