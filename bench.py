@@ -292,7 +292,7 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         else:
             blk = blk.to(device=dev, dtype=w.dtype).eval()
             # folded LayerNorms run inside the "qkv" / "ffn_in" stages (statistics pass included)
-            fold = blk.attention.folds_norm(w.dtype)
+            fold = blk.attention.folds_norm(w.dtype, x.numel())
             stages = ([] if fold else ["norm"]) + ["qkv", "attn", "out"] + \
                 ([] if fold else ["norm2"]) + ["ffn_in", "ffn_out"]
 
@@ -300,7 +300,7 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
             return block_forward(blk, x, valid, w.causal, marks=marks)
     elif half:
         norm = torch.nn.LayerNorm(w.d_model).to(device=dev, dtype=w.dtype)
-        if w.int8 or not mod.folds_norm(w.dtype):
+        if w.int8 or not mod.folds_norm(w.dtype, x.numel()):
             stages = ["norm"] + stages
 
         def step(marks=None):

@@ -164,8 +164,9 @@ def test_attention_half_is_the_unfused_composition(gpu, name, masked):
     xg = x.to(gpu)
     vg = None if valid is None else valid.to(gpu)
     if w.dtype == torch.float32:
-        # the fp32-operand path, whose unfused form is this composition; the default fp16
-        # operands of an fp32 model are judged against it below
+        # the fp32-operand path, whose unfused form is this composition; the fp16 operands an
+        # fp32 model takes at large inputs (forced here at every size) are judged against it below
+        mod.fp16_operand_min_elems = 0
         with torch.inference_mode():
             fp16_ops = mod.forward_residual(xg, norm, vg, w.causal)
         mod.fp32_operand_dtype = torch.float32

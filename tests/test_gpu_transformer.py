@@ -278,12 +278,16 @@ def test_official_shape14_full_length_causal_prefix(gpu, dtype):
     run must equal the same model run on the first 2048 tokens alone (bit for bit), and those are
     judged by the reference's predicate against the fp32 oracle model (fp32; the 16-bit model is
     checked block by block at this shape below). Every output is finite, and a batch row run
-    alone gives the same bits as in the full batch."""
+    alone gives the same bits as in the full batch. The fp32 model takes fp16 projection operands
+    only from a size on (SelfAttention.fp16_operand_min_elems), which the 2048-token prefix is
+    below: the threshold is pinned to 0 so all three runs take the full-length run's operands."""
     shape = OFFICIAL_SHAPES[13]
     cfg = _official_cfg(shape, 32, 100000)
     B, S, d, P = cfg.batch_size, cfg.seq_len, cfg.d_model, 2048
     print(f"official shape 14 full length dtype={dtype}: {cfg}", flush=True)
     baseline, model = _model(cfg, dtype, gpu, seed=1414)
+    for blk in model.layers:
+        blk.attention.fp16_operand_min_elems = 0
     g = torch.Generator(device=gpu).manual_seed(1414)
     x = torch.randn(B, S, d, device=gpu, generator=g).to(dtype)
     mask = torch.ones(B, S, dtype=torch.bool, device=gpu)

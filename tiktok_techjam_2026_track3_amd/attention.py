@@ -76,15 +76,21 @@ class SelfAttention(nn.Module):
     # runs fp32 models on fp16 tiles (Project/submission/dispatcher_region.py:1017-1091);
     # torch.float32 keeps fp32 operands (the LayerNorms then folded into the projections)
     fp32_operand_dtype = torch.float16
+    # ... from this many input elements on: below it the fp32 path (LayerNorm folded into
+    # 128 x 128-tile fp32 projections) is faster than a LayerNorm launch and 256 x 256-tile fp16
+    # projections that leave most CUs idle (official shapes 1, 5, 9, 10: 8192 x 128 tokens x
+    # features, 0.49-0.55 ms against 0.63-0.66 ms per forward)
+    fp16_operand_min_elems = 1 << 23
 
-    def operand_dtype(self, dtype: torch.dtype) -> torch.dtype:
+    def operand_dtype(self, dtype: torch.dtype, numel: int = 1 << 62) -> torch.dtype:
         """Operand dtype of the block's projections (forward_residual, the FFN half) for model
-        dtype ``dtype``."""
-        if dtype == torch.float32 and self.core_dtype(dtype) == torch.float16:
+        dtype ``dtype`` and an input of ``numel`` elements."""
+        if (dtype == torch.float32 and self.core_dtype(dtype) == torch.float16
+                and numel >= self.fp16_operand_min_elems):
             return self.fp32_operand_dtype
         return dtype
 
-    def folds_norm(self, dtype: torch.dtype) -> bool:
+    def folds_norm(self, dtype: torch.dtype, numel: int = 1 << 62) -> bool:
         """Whether forward_residual (and the block's FFN half) fold the LayerNorm for inputs of
         ``dtype``. bf16 keeps the LayerNorm kernel: the fold rounds gamma * W to bf16 where the
         reference rounds the normalised activations, and at bf16's 8-bit precision that moves
@@ -92,7 +98,7 @@ class SelfAttention(nn.Module):
         fp32 models on fp16 operands also run the LayerNorm kernel (fp32 statistics, fp16
         output): folding would round the raw x to fp16, whose mean need not be small."""
         return (bool(self.fold_norm) and dtype != torch.bfloat16
-                and self.operand_dtype(dtype) == dtype)
+                and self.operand_dtype(dtype, numel) == dtype)
 
     def __init__(self, d_model: int, num_heads: int) -> None:
         super().__init__()
@@ -281,13 +287,13 @@ class SelfAttention(nn.Module):
             if t is not None and (t.dtype != x.dtype or t.device != x.device):
                 raise ValueError("norm parameters must be on x's device in x's dtype")
         key_valid, row_valid = self._resolve_mask(valid_token_mask, B, S, x.device)
-        op = self.operand_dtype(x.dtype)
+        op = self.operand_dtype(x.dtype, x.numel())
         w_qkv, b_qkv, w_o, b_o = self._packed_weights(op, x.device)
         core = self.core_dtype(x.dtype)
         x2 = x.reshape(B * S, d)
         if not x2.is_contiguous():
             x2 = x2.contiguous()
-        if self.folds_norm(x.dtype):
+        if self.folds_norm(x.dtype, x.numel()):
             wf, colsum, bf = self._ln_folded_qkv(norm, x.dtype, x.device)
             mark("qkv")
             qkv = ops.layernorm_linear(x2, wf, colsum, bf, norm.eps, out_dtype=core)

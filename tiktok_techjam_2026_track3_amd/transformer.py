@@ -148,9 +148,9 @@ def block_forward(block: nn.Module, x: torch.Tensor, valid_token_mask: Optional[
     w2, b2 = _norm_params(block.norm2, x)
     # the FFN's operand dtype: the model's, or fp16 for fp32 models with an fp16 attention core
     # (SelfAttention.operand_dtype; the GELU output is then fp16 too, the residual stream fp32)
-    op = attn.operand_dtype(x.dtype)
+    op = attn.operand_dtype(x.dtype, x.numel())
     w_in, b_in, w_out, b_out = _ffn_weights(block, op, x.device)
-    if attn.folds_norm(x.dtype):
+    if attn.folds_norm(x.dtype, x.numel()):
         wf, colsum, bf = _ffn_in_folded(block, x.dtype, x.device)
         mark("ffn_in")
         g = ops.layernorm_linear(x1, wf, colsum, bf, block.norm2.eps, gelu=True)
