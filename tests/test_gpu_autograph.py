@@ -136,7 +136,7 @@ def test_forward_signatures_alternate(gpu):
 def test_large_inputs_and_outer_capture_stay_eager(gpu):
     dtype = torch.float16
     mod = _attn(gpu, dtype)
-    big = _x(gpu, dtype, B=2, S=4096)            # 2^21 elements: above the replay limit
+    big = _x(gpu, dtype, B=8, S=4096)            # 2^23 elements: above the replay limit
     x = _x(gpu, dtype)
     with torch.inference_mode():
         for _ in range(3):

@@ -102,8 +102,10 @@ class GraphedForward:
 
 # Input elements at or below which a module's forward replays a captured graph (AutoGraph): an
 # attention block of 128 x 256 (the fp32 configuration) spends ~18 us on the GPU against ~70 us
-# of host work per eager forward; at 2^20 elements the kernels' time already exceeds the host's.
-AUTO_GRAPH_MAX_ELEMS = 1 << 20
+# of host work per eager forward, and a 4-layer fp16 model of 128 x 128 x 128 (2^21 elements)
+# 0.41 ms against 0.50 ms of host work. Larger inputs keep the GPU busier than the host; the
+# replay's input copy and output clone grow with the input.
+AUTO_GRAPH_MAX_ELEMS = 1 << 22
 
 
 # Parameter or submodule registrations anywhere in the process (construction, replacement by
