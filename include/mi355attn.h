@@ -100,10 +100,16 @@ int mi355_attn_fwd(int dtype, const void* Q, const void* K, const void* V, void*
  * per-tile row maxima for the rest of its sweep: the output is bit-identical to mi355_attn_fwd.
  * Non-causal calls without a key mask: a wave whose bound keeps every score within +-8 (log2
  * units) from the start runs with mu = 0 and no row maxima at all (the max-free sweep); its
- * output then differs from mi355_attn_fwd only in rounding, under the same error bound.
- * workspace may be NULL (then the same as mi355_attn_fwd); a smaller non-NULL workspace is
- * MI355_E_BAD_SIZE. Causal calls with a key mask do not use it. The workspace is scratch: its
- * contents on return are unspecified, and calls that share one workspace must be stream-ordered.
+ * output then differs from mi355_attn_fwd only in rounding, under the same error bound. When
+ * the workspace also holds the redo flags (from the next 256-byte boundary after the bounds,
+ * one int per 256-query work-group: mi355_attn_workspace_bytes), a wave whose bounds exceed 8
+ * may instead fix mu at bound - 8 in advance (the offset sweep); a work-group in which a row's
+ * probability sum then stays below 1 is recomputed on the exact path by a second launch on the
+ * same stream. Same error bound.
+ * workspace may be NULL (then the same as mi355_attn_fwd); a smaller non-NULL workspace than
+ * the bounds need is MI355_E_BAD_SIZE. Causal calls with a key mask do not use it. The workspace
+ * is scratch: its contents on return are unspecified, and calls that share one workspace must
+ * be stream-ordered.
  */
 int mi355_attn_fwd_ws(int dtype, const void* Q, const void* K, const void* V, void* O, int64_t B,
                       int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim,
@@ -114,8 +120,9 @@ int mi355_attn_fwd_ws(int dtype, const void* Q, const void* K, const void* V, vo
 
 /*
  * Workspace bytes the library recommends for mi355_attn_fwd_ws on this problem: the key-norm
- * bound size when the problem runs on the matrix-core kernel with S_k >= 32768 (shorter key
- * ranges do not repay the extra pass over K), else 0 (call without a workspace).
+ * bounds rounded up to 256 bytes plus B * H * ceil(S_q / 256) redo flags of 4 bytes, when the
+ * problem runs on the matrix-core kernel with S_k >= 32768 (shorter key ranges do not repay
+ * the extra pass over K), else 0 (call without a workspace).
  */
 int64_t mi355_attn_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t S_q, int64_t S_k,
                                    int64_t head_dim);

@@ -128,16 +128,21 @@ def test_attention_argument_validation():
 
 def test_attention_workspace_argument_validation():
     """mi355_attn_fwd_ws: the recommended size is the key-norm bound array of the matrix-core
-    kernel (B * H * ceil(S_k / 1024) floats) from S_k = 32768 on, 0 elsewhere; a non-NULL
-    workspace below the bound size or misaligned is refused before any launch."""
+    kernel (B * H * ceil(S_k / 1024) floats), rounded up to 256 bytes, then one int per
+    work-group of 256 queries (the offset sweep's redo flags), from S_k = 32768 on, 0
+    elsewhere; a non-NULL workspace below the bound size or misaligned is refused before any
+    launch."""
     L = _lib()
     h = L.lib()
     codes = _status_codes()
     fake = 1 << 20
     B, H = 2, 4
-    assert h.mi355_attn_workspace_bytes(1, B, H, 32768, 32768, 64) == B * H * 32 * 4
-    assert h.mi355_attn_workspace_bytes(2, B, H, 10, 100000, 128) == B * H * 98 * 4
-    assert h.mi355_attn_workspace_bytes(1, B, H, 40000, 40000, 32) == B * H * 40 * 4
+
+    def size(S_q, S_k):
+        return (B * H * -(-S_k // 1024) * 4 + 255) // 256 * 256 + B * H * -(-S_q // 256) * 4
+    assert h.mi355_attn_workspace_bytes(1, B, H, 32768, 32768, 64) == size(32768, 32768) == 5120
+    assert h.mi355_attn_workspace_bytes(2, B, H, 10, 100000, 128) == size(10, 100000) == 3360
+    assert h.mi355_attn_workspace_bytes(1, B, H, 40000, 40000, 32) == size(40000, 40000) == 6304
     assert h.mi355_attn_workspace_bytes(1, B, H, 8192, 8192, 64) == 0      # short key range
     assert h.mi355_attn_workspace_bytes(0, B, H, 8192, 8192, 64) == 0      # fp32: VALU kernel
     assert h.mi355_attn_workspace_bytes(1, B, H, 8192, 8192, 80) == 0      # head_dim 80: VALU

@@ -369,15 +369,16 @@ def _bound_pair(gpu, dtype, B, H, S, hd, causal, scale_qk, seed, key_valid=None,
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
 @pytest.mark.parametrize("hd", [32, 64, 128])
-@pytest.mark.parametrize("causal,S,scale_qk", [(False, 100, 1.0), (True, 100, 1.0),
-                                              (False, 1500, 1.0), (True, 1500, 1.0),
+@pytest.mark.parametrize("causal,S,scale_qk", [(True, 100, 1.0), (True, 1500, 1.0),
                                               (True, 2600, None), (False, 1100, 3.0),
                                               (True, 1100, 3.0)])
 def test_attention_key_bound_bit_identical(gpu, dtype, hd, causal, S, scale_qk):
     """Where the workspace path keeps the exact running max, it skips a wave's row maxima only
     once the key-norm bound shows that mu can never move again, so its output equals the exact
     path's bit for bit: causal Q, K ~ N(0,1)/sqrt(head_dim) (the bound holds after the first
-    tile), N(0,1) (it holds for few waves) and large scores (never)."""
+    tile), N(0,1) (it holds for few waves) and large scores (never). Non-causal large scores
+    take the offset sweep, whose probabilities (~2^-40) fail its check in every work-group: the
+    redo launch gives the exact path's bits."""
     sc = hd ** -0.5 if scale_qk is None else scale_qk
     print(f"key bound dtype={dtype} hd={hd} causal={causal} S={S} scale={sc}", flush=True)
     a, b = _bound_pair(gpu, dtype, 2, 3, S, hd, causal, sc, 41)
@@ -400,15 +401,15 @@ def test_attention_max_free_sweep_against_oracle(gpu, dtype, hd, S):
 
 def test_attention_max_free_sweep_packed_and_mixed_heads(gpu):
     """Packed QKV views in the max-free sweep against the oracle; and a head whose keys are
-    large (bound above 8: exact path) beside heads in the max-free sweep: the large head is bit
-    for bit the exact path's, the others within the oracle bound."""
+    large (bound far above 8 + 256: neither sweep, the exact path) beside heads in the max-free
+    sweep: the large head is bit for bit the exact path's, the others within the oracle bound."""
     _attn_check(gpu, torch.float16, 2, 2, 1300, 1300, 64, False, packed=True, seed=48, qscale=0.125,
                 key_bound=True)
     ops = _ops()
     B, S, H, hd = 1, 3000, 3, 64
     q = _rand((B, S, H, hd), torch.float16, 71, scale=0.125)
     k = _rand((B, S, H, hd), torch.float16, 72, scale=0.125)
-    k[:, :, 2] = (k[:, :, 2].float() * 200).half()
+    k[:, :, 2] = (k[:, :, 2].float() * 2000).half()
     v = _rand((B, S, H, hd), torch.float16, 73)
     gq, gk, gv = q.to(gpu), k.to(gpu), v.to(gpu)
     a = ops.attention(gq, gk, gv, key_bound=False).cpu()
@@ -457,6 +458,96 @@ def test_attention_key_bound_nonfinite_and_huge_keys(gpu, bad):
     assert torch.equal(h1a[fin], h1b[fin])
     assert torch.isfinite(b[:, :, 0]).all()
     assert float((a[:, :, 0].float() - b[:, :, 0].float()).abs().max()) < 1e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hd", [32, 64, 128])
+@pytest.mark.parametrize("S", [100, 1500, 4097])
+def test_attention_offset_sweep_against_oracle(gpu, dtype, hd, S):
+    """Non-causal Q, K ~ N(0,1) (the block's projections): the bound exceeds 8, so the waves
+    run the offset sweep (mu fixed at bound - 8, no row maxima); work-groups whose row sums
+    pass the check keep it, the others are redone on the exact path. Checked against the oracle
+    under the exact path's error bound."""
+    _attn_check(gpu, dtype, 2, 3, S, S, hd, False, seed=49, key_bound=True)
+
+
+def _redo_flags_call(gpu, q, k, v):
+    """mi355_attn_fwd_ws with a workspace of the caller's (filled with 0x7f bytes); returns the
+    output and the workspace's ints after the 256-byte aligned bounds (the redo flags, one per
+    work-group of 256 queries, then the untouched fill)."""
+    from tiktok_techjam_2026_track3_amd import _lib as L
+    B, S, H, hd = q.shape
+    kb = B * H * ((S + 1023) // 1024) * 4
+    off = (kb + 255) // 256 * 256
+    n_wg = B * H * ((S + 255) // 256)
+    ws = torch.full((off + 4 * n_wg + 256,), 0x7F, device=gpu, dtype=torch.uint8)
+    out = torch.empty_like(q)
+    st = [L.i64_array((t.stride(0), t.stride(1), t.stride(2))) for t in (q, k, v, out)]
+    rc = L.lib().mi355_attn_fwd_ws(L.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
+                                   out.data_ptr(), B, H, S, S, hd, *st, hd ** -0.5, 0, None, 0,
+                                   ws.data_ptr(), ws.numel(), None)
+    L.check("mi355_attn_fwd_ws", rc)
+    torch.cuda.synchronize()
+    return out.cpu(), ws[off:].cpu().view(torch.int32), n_wg
+
+
+@pytest.mark.parametrize("hd", [32, 64, 128])
+def test_attention_offset_sweep_redo_flags(gpu, hd):
+    """The redo flags in the workspace. Large scores (Q, K ~ N(0, 9)): the first sub-tile's
+    maxima predict that the check would fail, so no wave takes the offset sweep: no flag, the
+    exact path's bits. Q, K ~ N(0,1) at head_dim 64 and S = 8192: work-groups keep the offset
+    sweep's results, so the output differs from the exact path's bits (their accuracy:
+    test_attention_offset_sweep_against_oracle). The flags after the work-groups' are
+    untouched."""
+    ops = _ops()
+    for scale, B, S, H in ((3.0, 2, 1500, 3), (1.0, 1, 8192, 2)):
+        q = _rand((B, S, H, hd), torch.float16, 301, scale=scale).to(gpu)
+        k = _rand((B, S, H, hd), torch.float16, 302, scale=scale).to(gpu)
+        v = _rand((B, S, H, hd), torch.float16, 303).to(gpu)
+        exact = ops.attention(q, k, v, key_bound=False).cpu()
+        out, flags, n_wg = _redo_flags_call(gpu, q, k, v)
+        print(f"hd={hd} scale={scale}: {int(flags[:n_wg].sum())} of {n_wg} work-groups redone",
+              flush=True)
+        assert torch.all(flags[n_wg:] == 0x7F7F7F7F)
+        assert torch.all((flags[:n_wg] == 0) | (flags[:n_wg] == 1))
+        if scale == 3.0:
+            assert torch.all(flags[:n_wg] == 0)
+            assert torch.equal(out, exact)
+        elif hd == 64:
+            assert torch.any(flags[:n_wg] == 0)
+            assert not torch.equal(out, exact)
+
+
+@pytest.mark.parametrize("hd", [32, 64, 128])
+def test_attention_offset_sweep_failed_check_is_redone(gpu, hd):
+    """A problem built so that the prediction passes and the check fails: every query points
+    along one unit vector u (|q| = sqrt(head_dim)); key 0 has norm L at cosine 0.83 to u, so the
+    first sub-tile's maximum a0 = 0.83 * |cq| * L lies within log2(S / 64) - 1 of mu0 =
+    1.0078 |cq| L + 1/128 - 8, and every other key is tiny (N(0, 0.01^2)), so the row sums come
+    to about 2^(a0 - mu0) < 1. Every work-group is flagged, and the redo launch gives the exact
+    path's bits."""
+    ops = _ops()
+    B, S, H = 1, 4096, 2
+    c = hd ** -0.5 * 1.4426950408889634
+    g = torch.Generator().manual_seed(307)
+    u = torch.randn(hd, generator=g)
+    u = u / u.norm()
+    w = torch.randn(hd, generator=g)
+    w = w - (w @ u) * u
+    w = w / w.norm()
+    qn = hd ** 0.5
+    L = 60.0 / (c * qn)                                    # bound ~ 60.5, mu0 ~ 52.5, a0 ~ 49.8
+    q = (u * qn).expand(B, S, H, hd).clone().half()
+    k = (torch.randn(B, S, H, hd, generator=g) * 0.01)
+    k[:, 0] = L * (0.83 * u + (1 - 0.83 ** 2) ** 0.5 * w)
+    k = k.half()
+    v = torch.randn(B, S, H, hd, generator=g).half()
+    q, k, v = q.to(gpu), k.to(gpu), v.to(gpu)
+    exact = ops.attention(q, k, v, key_bound=False).cpu()
+    out, flags, n_wg = _redo_flags_call(gpu, q, k, v)
+    print(f"hd={hd}: {int(flags[:n_wg].sum())} of {n_wg} work-groups redone", flush=True)
+    assert torch.all(flags[:n_wg] == 1)
+    assert torch.equal(out, exact)
 
 
 # ------------------------------------------------------------ all-true key mask (device check)

@@ -75,6 +75,8 @@ class SelfAttention(nn.Module):
     # in fp16, accumulation and the residual stream stay fp32 -- as the reference's fast route
     # runs fp32 models on fp16 tiles (Project/submission/dispatcher_region.py:1017-1091);
     # torch.float32 keeps fp32 operands (the LayerNorms then folded into the projections)
+    # key-mask length from which an all-true mask is checked on the host (_resolve_mask)
+    key_mask_check_min_seq = 32768
     fp32_operand_dtype = torch.float16
     # ... from this many input elements on: below it the fp32 path (LayerNorm folded into
     # 128 x 128-tile fp32 projections) is faster than a LayerNorm launch and 256 x 256-tile fp16
@@ -185,10 +187,12 @@ class SelfAttention(nn.Module):
     def _resolve_mask(self, mask: Optional[torch.Tensor], B: int, S: int, device: torch.device):
         """Returns (key_valid [B,S] bool or None, row_valid [B*S] bool or None).
 
-        A given mask always goes to the kernels: the attention kernel ballots the mask bytes of
-        each key tile and masks element-wise only where a tile holds invalid keys, so an
-        all-true mask costs one byte load per key per work-group and no host synchronisation
-        (unlike an "is it all true?" check on the host).
+        A given mask goes to the kernels: the attention kernel checks each work-group's mask
+        bytes on the device and masks element-wise only where a tile holds invalid keys, so an
+        all-true mask costs one byte load per key per work-group and no host synchronisation.
+        From ``key_mask_check_min_seq`` keys on (outside graph capture) an all-true mask is
+        recognised on the host instead and the attention runs without a key mask: there the
+        sync is small beside the launch, and only the unmasked kernel has the offset sweep.
         """
         if mask is None:
             return None, None
@@ -197,6 +201,9 @@ class SelfAttention(nn.Module):
         if mask.device != device:
             raise ValueError("valid_token_mask must be on the input's device")
         m = mask if mask.is_contiguous() else mask.contiguous()
+        if (S >= self.key_mask_check_min_seq and not torch.cuda.is_current_stream_capturing()
+                and bool(m.all())):
+            return None, m.view(B * S)
         return m, m.view(B * S)
 
     # ----------------------------------------------------------------------------- forward

@@ -49,6 +49,11 @@ struct AttnArgs {
   // i of head (b, h), written by attn_key_bound
   const float* kb;
   int kb_n;
+  // offset-sweep redo flags (nullable; non-causal MFMA launches without a key mask): one int per
+  // work-group (linear block index). The sweep launch writes every flag, 1 when a row of the
+  // work-group's offset sweep failed its check; the redo launch (the kernel's REDO instance)
+  // runs only the flagged work-groups, without the offset sweep.
+  int* redo;
 };
 
 // Keys per chunk of the key-norm bound pass.
@@ -65,6 +70,10 @@ constexpr bool KB_INSTANCE = !PIPE && !(CAUSAL && KMASK);
 // when every key is valid)
 template <bool PIPE, bool CAUSAL, bool KMASK>
 constexpr bool MAXFREE_INSTANCE = !PIPE && !CAUSAL && MI355_ATTN_MAXFREE;
+// ... and the offset sweep (instances without a key mask; the key-masked ones have no registers
+// to spare for it)
+template <bool PIPE, bool CAUSAL, bool KMASK>
+constexpr bool OFFSET_INSTANCE = MAXFREE_INSTANCE<PIPE, CAUSAL, KMASK> && !KMASK;
 
 constexpr float NEG_INF = -__builtin_huge_valf();
 
@@ -208,7 +217,7 @@ MI355_DEVINL float prob_sum16(const f16x8 (&f)[4]) {
 #endif
 
 template <typename T, int HD, int NW, int QG, int KT, int WPE, bool PRIO, bool PIPE, bool CAUSAL,
-          bool KMASK>
+          bool KMASK, bool REDO>
 __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   using MF = Mfma<T>;
   using frag = typename MF::frag;
@@ -244,6 +253,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
+  constexpr bool OFFSET = OFFSET_INSTANCE<PIPE, CAUSAL, KMASK> && !REDO;
+  const int64_t wg_id = blockIdx.x + static_cast<int64_t>(gridDim.x) *
+                                         (blockIdx.y + static_cast<int64_t>(gridDim.y) * blockIdx.z);
+  // the redo launch runs only the work-groups that the sweep launch flagged
+  if constexpr (REDO) {
+    if (p.redo[wg_id] == 0) return;
+  }
   int qt;
   int64_t h, b;
   tile_of_block<CAUSAL>(p, qt, h, b);
@@ -471,8 +487,18 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
     }
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
   };
-  // S^T of sub-tile j with mu = 0 (the max-free sweep): chains start from zero
-  auto score0 = [&](f32x16 (&sacc)[QG][2], const int st, const int k) MI355_LAMBDA_INLINE {
+  // S^T of sub-tile j in the max-free / offset sweep: chains start from -mu0 (0 in the
+  // max-free sweep; one value for all query groups of the lane), the block rebuilt per sub-tile
+  auto score0 = [&](f32x16 (&sacc)[QG][2], const int st, const int k, float mu0, auto off) MI355_LAMBDA_INLINE {
+    f32x16 z;
+    if constexpr (decltype(off)::value) {
+      asm volatile("" : "+v"(mu0));
+#pragma unroll
+      for (int i = 0; i < 16; ++i) z[i] = -mu0;
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) z[i] = 0.f;
+    }
 #pragma unroll
     for (int t = 0; t < 2; ++t) {
       frag kf[KS];
@@ -480,9 +506,6 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
       for (int s = 0; s < KS; ++s) kf[s] = kfrag(st, k, t, s);
 #pragma unroll
       for (int n = 0; n < QG; ++n) {
-        f32x16 z;
-#pragma unroll
-        for (int i = 0; i < 16; ++i) z[i] = 0.f;
         sacc[n][t] = MF::mma(kf[0], qf[n][0], z);
 #pragma unroll
         for (int s = 1; s < KS; ++s) sacc[n][t] = MF::mma(kf[s], qf[n][s], sacc[n][t]);
@@ -748,34 +771,88 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   // U stages per trip (a multiple of the ring depth, with an even sub-tile count when the score
   // buffers alternate) so every ring slot and buffer choice is a compile-time constant
   constexpr int U = PIPE ? ((KT % 2 == 0) ? 3 : 6) : NSTAGE;
+  // Largest offset of the offset sweep (log2 units): its score chains start from -mu0, so their
+  // fp32 rounding grows with mu0; at 2^8 it stays below 2^-15, far under the fp16 rounding of
+  // the probabilities.
+  constexpr float MU_MAX = 256.0f;
   int st = 0;
+  bool offset_sweep = false;  // this wave runs the offset sweep
   if constexpr (MAXFREE_INSTANCE<PIPE, CAUSAL, KMASK>) {
     // Max-free sweep: when the key-norm bound puts every score of the wave's queries within
     // [-thr, thr] (|s*c| <= |cq| max|k|), mu stays 0 for the whole sweep: probabilities lie in
-    // [2^-thr, 2^thr] and no row maximum is ever needed. The stages whose sub-tiles are all
-    // full and whose look-ahead loads are all in range run as one branch-free basic block
-    // (score chains from zero, exponentials, P.V), the rest through the generic stage below.
-    bool in_bound = use_kb && !kmask_live;
+    // [2^-thr, 2^thr] and no row maximum is ever needed.
+    // Offset sweep (otherwise; instances without a key mask, first launch, finite bounds up to
+    // thr + MU_MAX): mu is fixed in advance at mu0 = the larger bound - thr of the lane's two
+    // queries, which keeps every probability <= 2^thr as the running max would, with no row
+    // maxima either. Whether the probabilities came out large enough is checked at the end.
+    // The stages whose sub-tiles are all full and whose look-ahead loads are all in range run
+    // as one branch-free basic block (score chains from zero or -mu0, exponentials, P.V), the
+    // rest through the generic stage below.
+    bool in_bound = use_kb && !kmask_live, fixable = OFFSET && use_kb && p.redo;
+    float mu0 = 0.f;
 #pragma unroll
-    for (int n = 0; n < QG; ++n) in_bound = in_bound && qbound(n) <= thr;
-    if (use_kb && !kmask_live && __builtin_amdgcn_ballot_w64(!in_bound) == 0) {
+    for (int n = 0; n < QG; ++n) {
+      const float qb = qbound(n);
+      in_bound = in_bound && qb <= thr;
+      fixable = fixable && qb - thr <= MU_MAX;  // false for NaN / inf bounds
+      mu0 = vmax(mu0, qb - thr);
+    }
+    const bool all_in = use_kb && !kmask_live && __builtin_amdgcn_ballot_w64(!in_bound) == 0;
+    bool offset = OFFSET && use_kb && !all_in && __builtin_amdgcn_ballot_w64(!fixable) == 0;
+    if constexpr (OFFSET) {
+      if (offset) {
+        // Prediction of the check: the row sums of the first sub-tile (in LDS already) at the
+        // offset, times the n_kt sub-tiles, estimate the final sums; waves whose estimate is
+        // below 4 keep the exact path instead of paying for a sweep and its redo (large
+        // score ranges, short key ranges).
+        score0(s_a, 0, 0, mu0, std::integral_constant<bool, OFFSET>{});
+        bool near = true;
+#pragma unroll
+        for (int n = 0; n < QG; ++n) {
+          float sum = 0.f;
+#pragma unroll
+          for (int t = 0; t < 2; ++t)
+#pragma unroll
+            for (int i = 0; i < 16; ++i) sum += fast_exp2(s_a[n][t][i]);
+          near = near && pair_sum(sum) * static_cast<float>(n_kt) >= 4.0f;
+        }
+        offset = __builtin_amdgcn_ballot_w64(!near) == 0;
+      }
+    }
+    offset_sweep = offset;
+    if (all_in || offset) {
       nomax = true;
       const int full_st = Sk / (KT * BN);
       const int load_st = n_kt / KT - NSTAGE + 1;
       const int n_main = full_st < load_st ? full_st : load_st;
-      auto stage_mf = [&](const int stg, const int cur, const int far) MI355_LAMBDA_INLINE {
+      auto run_mf = [&](auto off) MI355_LAMBDA_INLINE {
+        auto stage_mf = [&](const int stg, const int cur, const int far) MI355_LAMBDA_INLINE {
 #pragma unroll
-        for (int k = 0; k < KT; ++k) {
-          issue_loads(stg * KT + k + (NSTAGE - 1) * KT, far, k);
-          score0(s_a, cur, k);
-          exp_pv(s_a, cur, k);
+          for (int k = 0; k < KT; ++k) {
+            issue_loads(stg * KT + k + (NSTAGE - 1) * KT, far, k);
+            score0(s_a, cur, k, mu0, off);
+            exp_pv(s_a, cur, k);
+          }
+          __builtin_amdgcn_s_waitcnt(0);  // this wave's loads into slot far have landed
+          __syncthreads();
+        };
+        for (; st + U - 1 < n_main; st += U) {
+#pragma unroll
+          for (int u = 0; u < U; ++u) stage_mf(st + u, u % NSTAGE, (u + NSTAGE - 1) % NSTAGE);
         }
-        __builtin_amdgcn_s_waitcnt(0);  // this wave's loads into slot far have landed
-        __syncthreads();
       };
-      for (; st + U - 1 < n_main; st += U) {
+      if (!offset) {
+        run_mf(std::false_type{});
+      } else {
+        run_mf(std::integral_constant<bool, OFFSET>{});
+      }
+      if (offset) {
 #pragma unroll
-        for (int u = 0; u < U; ++u) stage_mf(st + u, u % NSTAGE, (u + NSTAGE - 1) % NSTAGE);
+        for (int n = 0; n < QG; ++n) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) negmu[n][i] = -mu0;
+          gate[n] = thr;
+        }
       }
     }
   }
@@ -788,6 +865,23 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   for (int u = 0; u < U - 1; ++u)
     if (st + u < n_st)
       stage(st + u, u % NSTAGE, (u + 1) % NSTAGE, (u + NSTAGE - 1) % NSTAGE, (u * KT) & 1);
+
+  // The offset sweep's check: every row sum of the work-group's queries at least 1 (the exact
+  // path's maximum alone contributes 1), so that no more of a row's probabilities fall below
+  // fp16's normal range than on the exact path; a NaN sum fails it too. A failed work-group is
+  // flagged for the redo launch, which overwrites its output from the exact path.
+  if constexpr (OFFSET) {
+    if (p.redo != nullptr) {
+      bool low = false;
+#pragma unroll
+      for (int n = 0; n < QG; ++n) {
+        const float tot = pair_sum(lsum[n]);
+        low = low || (offset_sweep && q_wave + 32 * n + l32 < p.Sq && !(tot >= 1.0f));
+      }
+      const int bad = __syncthreads_or(low);
+      if (tid == 0) p.redo[wg_id] = bad != 0 ? 1 : 0;
+    }
+  }
 
   // Epilogue. Each lane holds, per query group, 4-element runs of its query's output row; the
   // wave stages its QW x HD tile, divided by the row sums and rounded to T, in LDS (the K / V
@@ -1171,17 +1265,17 @@ __global__ __launch_bounds__(64 * NWK) void attn_fwd_valu(AttnArgs p) {
 #endif
 
 
-template <typename T, int HD, int NW, int QG, bool CAUSAL, bool KMASK>
+template <typename T, int HD, int NW, int QG, bool CAUSAL, bool KMASK, bool REDO = false>
 void launch_one(const AttnArgs& a, dim3 grid, dim3 block, hipStream_t s) {
   constexpr int KT = HD <= 64 ? MI355_ATTN_KT64 : MI355_ATTN_KT128;
   constexpr int WPE = HD <= 64 ? MI355_ATTN_WPE64 : MI355_ATTN_WPE128;
   constexpr bool PRIO = (HD <= 64 ? MI355_ATTN_PRIO64 : MI355_ATTN_PRIO128) != 0;
   constexpr bool PIPE = HD == 64 && (!KMASK || MI355_ATTN_PIPE64 > 1) && MI355_ATTN_PIPE64 != 0;
-  hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, KT, WPE, PRIO, PIPE, CAUSAL, KMASK>), grid, block, 0, s, a);
+  hipLaunchKernelGGL((attn_fwd_mfma<T, HD, NW, QG, KT, WPE, PRIO, PIPE, CAUSAL, KMASK, REDO>), grid, block, 0, s, a);
 }
 
 template <typename T, int HD, int NW, int QG>
-int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, float* kb_ws, hipStream_t s) {
+int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, float* kb_ws, int* redo, hipStream_t s) {
   AttnArgs a = a0;
   if (kb_ws && !(causal && kmask)) {
     // the key-norm bounds of every head, read by the attention kernel's prologue
@@ -1201,9 +1295,13 @@ int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, float* kb_ws, hipSt
   if (causal) {
     if (kmask) launch_one<T, HD, NW, QG, true, true>(a, grid, block, s);
     else launch_one<T, HD, NW, QG, true, false>(a, grid, block, s);
+  } else if (kmask) {
+    launch_one<T, HD, NW, QG, false, true>(a, grid, block, s);
   } else {
-    if (kmask) launch_one<T, HD, NW, QG, false, true>(a, grid, block, s);
-    else launch_one<T, HD, NW, QG, false, false>(a, grid, block, s);
+    // with redo flags: the offset sweep may run, then the flagged work-groups again
+    a.redo = a.kb ? redo : nullptr;
+    launch_one<T, HD, NW, QG, false, false>(a, grid, block, s);
+    if (a.redo) launch_one<T, HD, NW, QG, false, false, true>(a, grid, block, s);
   }
   return static_cast<int>(hipGetLastError());
 }
@@ -1292,6 +1390,23 @@ int64_t key_bound_bytes(int64_t B, int64_t H, int64_t S_k) {
   return B * H * ((S_k + KB_CHUNK - 1) / KB_CHUNK) * static_cast<int64_t>(sizeof(float));
 }
 
+// Queries per work-group of the MFMA kernel at this head_dim.
+int64_t mfma_block_queries(int64_t head_dim) {
+  if (head_dim == 32) return MI355_ATTN_NW32 * 32 * MI355_ATTN_QG32;
+  if (head_dim == 64) return MI355_ATTN_NW64 * 32 * MI355_ATTN_QG64;
+  return MI355_ATTN_NW128 * 32 * MI355_ATTN_QG128;
+}
+
+// Workspace layout: key-norm bounds, then (from the next 256-byte boundary) one redo flag per
+// work-group of the attention launch.
+int64_t redo_offset(int64_t B, int64_t H, int64_t S_k) {
+  return (key_bound_bytes(B, H, S_k) + 255) / 256 * 256;
+}
+int64_t redo_flag_bytes(int64_t B, int64_t H, int64_t S_q, int64_t head_dim) {
+  const int64_t bm = mfma_block_queries(head_dim);
+  return B * H * ((S_q + bm - 1) / bm) * static_cast<int64_t>(sizeof(int));
+}
+
 int attn_fwd_impl(int dtype, const void* Q, const void* K, const void* V, void* O, int64_t B,
                   int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim, const int64_t* q_strides,
                   const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
@@ -1352,24 +1467,28 @@ int attn_fwd_impl(int dtype, const void* Q, const void* K, const void* V, void* 
                               : dispatch_valu<__bf16>(a, head_dim, cz, kmask, s);
   }
   float* kb = nullptr;
+  int* redo = nullptr;
   if (workspace != nullptr && S_k > 0) {
     if (workspace_bytes < key_bound_bytes(B, H, S_k)) return MI355_E_BAD_SIZE;
     if (reinterpret_cast<uintptr_t>(workspace) & 3u) return MI355_E_ALIGNMENT;
     if ((S_k + KB_CHUNK - 1) / KB_CHUNK > 0x7fffffff) return MI355_E_BAD_SIZE;
     kb = static_cast<float*>(workspace);
+    // room for the redo flags as well: the offset sweep is allowed
+    if (workspace_bytes >= redo_offset(B, H, S_k) + redo_flag_bytes(B, H, S_q, head_dim))
+      redo = reinterpret_cast<int*>(static_cast<char*>(workspace) + redo_offset(B, H, S_k));
   }
   if (dtype == MI355_F16) {
     if (head_dim == 32)
-      return launch_mfma<_Float16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, kb, s);
+      return launch_mfma<_Float16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, kb, redo, s);
     return head_dim == 64
-               ? launch_mfma<_Float16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, kb, s)
-               : launch_mfma<_Float16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, kb, s);
+               ? launch_mfma<_Float16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, kb, redo, s)
+               : launch_mfma<_Float16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, kb, redo, s);
   }
   if (head_dim == 32)
-    return launch_mfma<__bf16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, kb, s);
+    return launch_mfma<__bf16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, kb, redo, s);
   return head_dim == 64
-             ? launch_mfma<__bf16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, kb, s)
-             : launch_mfma<__bf16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, kb, s);
+             ? launch_mfma<__bf16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, kb, redo, s)
+             : launch_mfma<__bf16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, kb, redo, s);
 }
 
 }  // namespace
@@ -1387,9 +1506,9 @@ extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const voi
 
 extern "C" int64_t mi355_attn_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t S_q,
                                               int64_t S_k, int64_t head_dim) {
-  (void)S_q;
-  if (B <= 0 || H <= 0 || S_k < MI355_ATTN_KB_MIN_SK || !on_mfma_kernel(dtype, head_dim)) return 0;
-  return key_bound_bytes(B, H, S_k);
+  if (B <= 0 || H <= 0 || S_q <= 0 || S_k < MI355_ATTN_KB_MIN_SK || !on_mfma_kernel(dtype, head_dim))
+    return 0;
+  return redo_offset(B, H, S_k) + redo_flag_bytes(B, H, S_q, head_dim);
 }
 
 extern "C" int mi355_attn_fwd_ws(int dtype, const void* Q, const void* K, const void* V, void* O,

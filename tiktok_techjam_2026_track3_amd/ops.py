@@ -227,8 +227,9 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[t
     ``view(B, S_q, H * head_dim)`` is the merged-head context of the reference block.
     ``key_valid`` is an optional ``[B, S_k]`` bool mask of keys to attend to.
     ``key_bound`` selects the key-norm bound pass of the matrix-core kernel (a workspace of
-    per-chunk max |k| that lets waves skip the per-tile row maxima): None = the library's
-    choice (``mi355_attn_workspace_bytes``: long key ranges), True = always, False = never.
+    per-chunk max |k| that lets waves skip the per-tile row maxima, and of the offset sweep's
+    redo flags): None = the library's choice (``mi355_attn_workspace_bytes``: long key
+    ranges), True = always, False = never.
     """
     _on_gpu(q, k, v, out, key_valid)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
@@ -257,7 +258,9 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[t
     if key_bound is None:
         ws_bytes = L.lib().mi355_attn_workspace_bytes(code, B, H, Sq, Sk, D)
     elif key_bound and dt != torch.float32 and D in (32, 64, 128):
-        ws_bytes = B * H * ((Sk + 1023) // 1024) * 4
+        # the per-chunk bounds, then (256-byte aligned) the offset sweep's redo flags: one per
+        # work-group of at least 32 queries
+        ws_bytes = (B * H * ((Sk + 1023) // 1024) * 4 + 255) // 256 * 256 + B * H * ((Sq + 31) // 32) * 4
     else:
         ws_bytes = 0
     args = (code, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq, Sk, D,
