@@ -487,12 +487,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
     }
     if constexpr (PRIO) __builtin_amdgcn_s_setprio(0);
   };
-  // S^T of sub-tile j in the max-free / offset sweep: chains start from -mu0 (0 in the
-  // max-free sweep; one value for all query groups of the lane), the block rebuilt per sub-tile
+  // S^T of sub-tile j in the max-free / offset sweep: chains start from -mu0 (the literal 0 in
+  // the max-free sweep; in the offset sweep one 16-register block for all query groups)
   auto score0 = [&](f32x16 (&sacc)[QG][2], const int st, const int k, float mu0, auto off) MI355_LAMBDA_INLINE {
     f32x16 z;
     if constexpr (decltype(off)::value) {
-      asm volatile("" : "+v"(mu0));
 #pragma unroll
       for (int i = 0; i < 16; ++i) z[i] = -mu0;
     } else {
