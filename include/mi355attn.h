@@ -98,8 +98,9 @@ int mi355_attn_fwd(int dtype, const void* Q, const void* K, const void* V, void*
  * before the attention launch. A wave whose every query satisfies |c q| max|k| - mu <= 8 (c =
  * scale * log2 e, mu its lazily moved running maximum) can never move mu again, so it skips the
  * per-tile row maxima for the rest of its sweep: the output is bit-identical to mi355_attn_fwd.
- * Non-causal calls without a key mask: a wave whose bound keeps every score within +-8 (log2
- * units) from the start runs with mu = 0 and no row maxima at all (the max-free sweep); its
+ * Calls without a key mask (causal ones over the keys before each 256-query work-group's first
+ * query): a wave whose bound keeps every score within +-8 (log2 units) from the start runs with
+ * mu = 0 and no row maxima at all (the max-free sweep); its
  * output then differs from mi355_attn_fwd only in rounding, under the same error bound. When
  * the workspace also holds the redo flags (from the next 256-byte boundary after the bounds,
  * one int per 256-query work-group: mi355_attn_workspace_bytes), a wave whose bounds exceed 8

@@ -277,8 +277,11 @@ def test_official_shape14_full_length_causal_prefix(gpu, dtype):
     output rows [0, P) depend only on input rows [0, P): the first 2048 rows of the full-length
     run must equal the same model run on the first 2048 tokens alone (bit for bit), and those are
     judged by the reference's predicate against the fp32 oracle model (fp32; the 16-bit model is
-    checked block by block at this shape below). Every output is finite, and a batch row run
-    alone gives the same bits as in the full batch. The fp32 model takes fp16 projection operands
+    checked block by block at this shape below). The prefix property is checked with the exact
+    running max (key_bound False: the sweeps' offsets depend on the bounds of all keys), and
+    the default run (the library's max-free / offset sweeps) against it by the predicate on
+    2 x 16384 rows. Every output is finite, and a batch row run alone gives the same bits as in
+    the full batch. The fp32 model takes fp16 projection operands
     only from a size on (SelfAttention.fp16_operand_min_elems), which the 2048-token prefix is
     below: the threshold is pinned to 0 so all three runs take the full-length run's operands."""
     shape = OFFICIAL_SHAPES[13]
@@ -291,15 +294,24 @@ def test_official_shape14_full_length_causal_prefix(gpu, dtype):
     g = torch.Generator(device=gpu).manual_seed(1414)
     x = torch.randn(B, S, d, device=gpu, generator=g).to(dtype)
     mask = torch.ones(B, S, dtype=torch.bool, device=gpu)
+    rows = [0, B - 1]
     with torch.inference_mode():
         out = model(x, mask)
         assert torch.isfinite(out).all()
-        rows = [0, B - 1]
-        prefix = model(x[rows, :P].contiguous(), mask[rows, :P].contiguous())
-        assert torch.equal(prefix, out[rows, :P])
         alone = model(x[B - 1:B].contiguous(), mask[B - 1:B].contiguous())
         assert torch.equal(alone[0], out[B - 1])
-    del out, alone
+        del alone
+        # the exact running max (no key-norm bound workspace): the prefix property bit for bit
+        for blk in model.layers:
+            blk.attention.key_bound = False
+        exact = model(x, mask)
+        prefix = model(x[rows, :P].contiguous(), mask[rows, :P].contiguous())
+        assert torch.equal(prefix, exact[rows, :P])
+        # the default full-length run (max-free / offset sweeps at this length) against it
+        r = compare_outputs(exact[rows, :16384].float().cpu(), out[rows, :16384].float().cpu())
+        print("  default vs exact running max, 2 x 16384 rows:", r.summary(), flush=True)
+        assert r.passed, r.summary()
+    del out, exact
     if dtype == torch.float32:
         ref = baseline(x[rows, :P].cpu(), torch.ones(len(rows), P, dtype=torch.bool))
         r = compare_outputs(ref, prefix.cpu())

@@ -77,6 +77,9 @@ class SelfAttention(nn.Module):
     # torch.float32 keeps fp32 operands (the LayerNorms then folded into the projections)
     # key-mask length from which an all-true mask is checked on the host (_resolve_mask)
     key_mask_check_min_seq = 32768
+    # the attention kernel's key-norm bound workspace (ops.attention): None = the library's
+    # choice (long key ranges: the max-free and offset sweeps), False = the exact running max
+    key_bound: Optional[bool] = None
     fp32_operand_dtype = torch.float16
     # ... from this many input elements on: below it the fp32 path (LayerNorm folded into
     # 128 x 128-tile fp32 projections) is faster than a LayerNorm launch and 256 x 256-tile fp16
@@ -258,7 +261,8 @@ class SelfAttention(nn.Module):
         qkv = ops.linear(x2, w_qkv, b_qkv, out_dtype=core)
         q, k, v = self._qkv_views(qkv, B, S)
         mark("attn")
-        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid)
+        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid,
+                                key_bound=self.key_bound)
         mark("out")
         out = ops.linear(ctx.view(B * S, d), w_o, b_o, row_valid=row_valid, out_dtype=x.dtype)
         mark("end")
@@ -312,7 +316,8 @@ class SelfAttention(nn.Module):
             qkv = ops.linear(h, w_qkv, b_qkv, out_dtype=core)
         q, k, v = self._qkv_views(qkv, B, S)
         mark("attn")
-        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid)
+        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid,
+                                key_bound=self.key_bound)
         mark("out")
         out = ops.linear(ctx.view(B * S, d), w_o, b_o, row_valid=row_valid, out_dtype=x.dtype,
                          residual=x2)
@@ -361,7 +366,8 @@ class Int8SelfAttention(SelfAttention):
         qkv = ops.linear_i8(xq, wq, sx, s_qkv, b_qkv, out_dtype=torch.float16)
         q, k, v = self._qkv_views(qkv, B, S)
         mark("attn")
-        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid)
+        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid,
+                                key_bound=self.key_bound)
         mark("quant_ctx")
         cq, sc = ops.quant_rows_i8(ctx.view(B * S, d), mode=0)
         mark("out")
@@ -405,7 +411,8 @@ class Int8SelfAttention(SelfAttention):
         qkv = ops.linear_i8(hq, wq, sh, s_qkv, b_qkv, out_dtype=torch.float16)
         q, k, v = self._qkv_views(qkv, B, S)
         mark("attn")
-        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid)
+        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid,
+                                key_bound=self.key_bound)
         mark("quant_ctx")
         cq, sc = ops.quant_rows_i8(ctx.view(B * S, d), mode=0)
         mark("out")

@@ -66,10 +66,11 @@ constexpr int KB_CHUNK = 1024;
 // MFMA kernel instances that take key-norm bounds
 template <bool PIPE, bool CAUSAL, bool KMASK>
 constexpr bool KB_INSTANCE = !PIPE && !(CAUSAL && KMASK);
-// ... and that run the max-free sweep when the bound allows it (non-causal; with a key mask only
-// when every key is valid)
+// ... and that run the max-free sweep when the bound allows it (non-causal, with a key mask only
+// when every key is valid; causal without a key mask, over the keys before the work-group's
+// first query)
 template <bool PIPE, bool CAUSAL, bool KMASK>
-constexpr bool MAXFREE_INSTANCE = !PIPE && !CAUSAL && MI355_ATTN_MAXFREE;
+constexpr bool MAXFREE_INSTANCE = !PIPE && !(CAUSAL && KMASK) && MI355_ATTN_MAXFREE;
 // ... and the offset sweep (instances without a key mask; the key-masked ones have no registers
 // to spare for it)
 template <bool PIPE, bool CAUSAL, bool KMASK>
@@ -821,7 +822,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
     offset_sweep = offset;
     if (all_in || offset) {
       nomax = true;
-      const int full_st = Sk / (KT * BN);
+      // (causal: the keys before the work-group's first query, visible to all its queries)
+      const int full_st = (CAUSAL ? (q_wg < Sk ? static_cast<int>(q_wg) : Sk) : Sk) / (KT * BN);
       const int load_st = n_kt / KT - NSTAGE + 1;
       const int n_main = full_st < load_st ? full_st : load_st;
       auto run_mf = [&](auto off) MI355_LAMBDA_INLINE {
@@ -1292,8 +1294,13 @@ int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, float* kb_ws, int* 
   if (causal && !flat) return MI355_E_BAD_SIZE;
   if (flat) grid = dim3(static_cast<unsigned>(n), 1, 1);
   if (causal) {
-    if (kmask) launch_one<T, HD, NW, QG, true, true>(a, grid, block, s);
-    else launch_one<T, HD, NW, QG, true, false>(a, grid, block, s);
+    if (kmask) {
+      launch_one<T, HD, NW, QG, true, true>(a, grid, block, s);
+    } else {
+      a.redo = a.kb ? redo : nullptr;
+      launch_one<T, HD, NW, QG, true, false>(a, grid, block, s);
+      if (a.redo) launch_one<T, HD, NW, QG, true, false, true>(a, grid, block, s);
+    }
   } else if (kmask) {
     launch_one<T, HD, NW, QG, false, true>(a, grid, block, s);
   } else {
