@@ -275,6 +275,12 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   // row strides in bytes; the entry point guarantees 64 rows of them fit in 32 bits
   const uint32_t kstride = static_cast<uint32_t>(p.ks1) * sizeof(T);
   const uint32_t vstride = static_cast<uint32_t>(p.vs1) * sizeof(T);
+  // K / V head bases as wave-uniform (scalar) values, so that each sub-tile's buffer descriptor
+  // is built on the scalar unit
+  const char* __restrict__ Kbs = uniform_ptr(Kb);
+  const char* __restrict__ Vbs = uniform_ptr(Vb);
+  // most rows whose bytes still fit a 32-bit buffer range
+  const uint32_t kcap = 0xffffffffu / kstride, vcap = 0xffffffffu / vstride;
 
   // Q^T fragments pre-scaled by c: group n, lane (query q_wave + 32n + l32, slice g) holds
   // c * Q[q][16*s + 8*g .. +7].
@@ -385,12 +391,13 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
         dma_lds1(kvb + ((k0 + lane < Sk) ? k0 + lane : Sk - 1), lds_addr_of(&kv_lds[s][k][0]));
     }
 #if MI355_ATTN_BUFLOAD
-    const uint64_t krem = static_cast<uint64_t>(Sk - k0) * kstride;
-    const uint64_t vrem = static_cast<uint64_t>(Sk - k0) * vstride;
-    const u32x4 kr = buffer_rsrc(Kb + static_cast<uint64_t>(k0) * kstride,
-                                 krem > 0xffffffffull ? 0xffffffffu : static_cast<uint32_t>(krem));
-    const u32x4 vr = buffer_rsrc(Vb + static_cast<uint64_t>(k0) * vstride,
-                                 vrem > 0xffffffffull ? 0xffffffffu : static_cast<uint32_t>(vrem));
+    // (32 x 32 -> 64-bit products and 32-bit clamps, so that the wave-uniform descriptor
+    // arithmetic stays on the scalar unit; k0 < Sk for every call)
+    const uint32_t rem = static_cast<uint32_t>(Sk - k0);
+    const u32x4 kr = buffer_rsrc(Kbs + static_cast<uint64_t>(static_cast<uint32_t>(k0)) * kstride,
+                                 rem > kcap ? 0xffffffffu : rem * kstride);
+    const u32x4 vr = buffer_rsrc(Vbs + static_cast<uint64_t>(static_cast<uint32_t>(k0)) * vstride,
+                                 rem > vcap ? 0xffffffffu : rem * vstride);
 #endif
 #pragma unroll
     for (int i = 0; i < LPW; ++i) {

@@ -127,6 +127,14 @@ MI355_DEVINL void dma_lds1(const void* gptr, uint32_t lds_addr) {
                "s"(__builtin_amdgcn_readfirstlane(lds_addr))
                : "memory", "m0");
 }
+// A wave-uniform pointer held in scalar registers (the value of the wave's first lane).
+template <typename P>
+MI355_DEVINL P* uniform_ptr(P* ptr) {
+  const uint64_t a = reinterpret_cast<uint64_t>(ptr);
+  const uint64_t lo = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a)));
+  const uint64_t hi = static_cast<uint32_t>(__builtin_amdgcn_readfirstlane(static_cast<uint32_t>(a >> 32)));
+  return reinterpret_cast<P*>(lo | (hi << 32));
+}
 // Raw buffer resource (base, stride 0, `bytes` records, 32-bit data format) as four wave-uniform
 // dwords: loads at or past `bytes` (voffset + soffset + instruction offset) return zeros.
 MI355_DEVINL u32x4 buffer_rsrc(const void* base, uint32_t bytes) {
