@@ -90,17 +90,33 @@ def parse_args():
 
 
 TRAFFIC_FILE = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "traffic.json")
-STAGE_KERNEL = {"qkv": "gemm_kernel", "attn": "attn_fwd", "out": "gemm_kernel"}
 
 
-def measured_traffic(config: str, stage: str):
-    """HBM bytes per launch of the stage's kernel from the committed counter runs, or None."""
+def stage_kernels(w, stage: str, core_dtype):
+    """Kernel families the stage launches on this build: the attention stage runs the matrix-core
+    kernel (with its key-norm bound pass) for 16-bit cores at head dims 32 / 64 / 128, else the
+    vector-ALU kernel; the projections run the GEMM kernels."""
+    import torch
+    if stage == "attn":
+        if core_dtype in (torch.float16, torch.bfloat16) and w.head_dim in (32, 64, 128):
+            return ("attn_fwd_mfma", "attn_key_bound")
+        return ("attn_fwd_valu",)
+    return ("gemm_kernel", "gemm_splitk", "gemm_f32_splitk", "layernorm_stats")
+
+
+def measured_traffic(config: str, stage: str, families) -> dict:
+    """HBM bytes per call of the stage from the committed counter runs (profiles/traffic.json),
+    or None when the record is missing or was measured on kernels of another family (every
+    kernel it summed must be one of ``families``, and the first of them among them)."""
     try:
         with open(TRAFFIC_FILE) as f:
             rec = json.load(f).get(config)
     except (OSError, ValueError):
         return None
-    if not rec or stage not in STAGE_KERNEL or STAGE_KERNEL[stage] not in rec.get("kernel", ""):
+    if not rec or rec.get("stage") != stage:
+        return None
+    names = [k.split("<")[0] for k in rec.get("kernels", {})]
+    if not names or any(n not in families for n in names) or families[0] not in names:
         return None
     return rec["bytes_per_launch"]
 
@@ -156,14 +172,45 @@ def host_cores() -> dict:
 
 
 # ------------------------------------------------------------------------------- cpu baseline
-def cpu_baseline(w, budget_s: float, core: bool = False) -> dict:
-    """Times the CPU oracle (the reference path restated in torch-CPU fp32) on a bounded sample
-    of one batch row: the QKV projection of all its tokens (the keys and values every query
-    needs), attention for ``n_q`` query rows spread over the sequence (the whole row when it is
-    short), and the output projection of those rows; ``core`` times the attention of those rows
-    alone on the core's own inputs. Every core this process may use (capped by the cgroup CPU
-    quota) runs torch's CPU kernels. Reports the operation rate in the metric's unit."""
+def _time_calls(fn, budget_s: float, max_calls: int = 500):
+    """Median seconds per call of ``fn`` (time.perf_counter_ns around each call, as the
+    reference's CPU branch, torch_transformer_benchmark.py:501-506): about ``budget_s`` of
+    calls, at least 3; the first call is dropped when more than one ran (one-time costs)."""
+    times = []
+    t_all = time.perf_counter()
+    while True:
+        t0 = time.perf_counter_ns()
+        fn()
+        times.append((time.perf_counter_ns() - t0) / 1e9)
+        if (time.perf_counter() - t_all > budget_s and len(times) >= 3) or len(times) >= max_calls:
+            break
+    timed = sorted(times[1:] if len(times) > 1 else times)
+    return timed[len(timed) // 2], len(timed), len(times)
+
+
+def cpu_baseline(w, budget_s: float, core: bool = False, gpu_eval=None) -> dict:
+    """Times the CPU oracle (the reference path restated in torch-CPU fp32; the int8 recipe in
+    numpy for C4) stage by stage on a bounded sample of one batch row, and composes the
+    full-workload CPU time from the stage rates:
+
+    * ``qkv``: the QKV projection of all S tokens of the row (the keys and values every query
+      needs), times B for the whole batch;
+    * ``attn``: the attention of ``n_q`` query rows of that row (all of them when S <= 4096,
+      else 256 spread over the sequence), all heads, times (full query-key pairs / sampled
+      pairs);
+    * ``out``: the output projection of those rows, times T / n_q.
+
+    ``core`` times the attention stage alone on the core's own inputs. ``ms_per_iter_extrapolated``
+    is the sum of the scaled stage times (labelled extrapolated wherever a multiplier exceeds 1);
+    ``value`` is the whole workload's operation count over it, in the metric's unit. Every core
+    this process may use (capped by the cgroup CPU quota) runs torch's CPU kernels.
+
+    ``gpu_eval`` (the GPU path on the same sample input) adds ``parity``: the reference's
+    predicate (torch_transformer_benchmark.py:306-316) of the GPU output rows against the
+    oracle's, with the fraction of elements that pass (C4: against the int8 recipe)."""
+    import numpy as np
     import torch
+    import torch.nn.functional as F
     from oracle import attention as OA
     from oracle import int8 as OI
     from oracle import streamed as OS
@@ -174,64 +221,105 @@ def cpu_baseline(w, budget_s: float, core: bool = False) -> dict:
     if hc["cgroup_quota_cpus"]:
         threads = min(threads, hc["cgroup_quota_cpus"])
     torch.set_num_threads(threads)
-    S, d, H, hd = w.seq, w.d_model, w.heads, w.head_dim
+    B, S, d, H, hd = w.batch, w.seq, w.d_model, w.heads, w.head_dim
+    T = w.tokens
     row = w.scaled(batch=1)
     n_q = S if S <= 4096 else 256
     idx = torch.linspace(0, S - 1, n_q).round().long() if n_q < S else torch.arange(S)
-    attn_pairs = float(((idx + 1).sum() if w.causal else n_q * S))
-    if core:
-        q, k, v = (t.float().permute(0, 2, 1, 3).contiguous()
-                   for t in W.make_core_inputs(row, W.TIMING_SEED))
-
-        def one():
-            return OS.streamed_attention_core(q[:, :, idx], k, v, hd ** -0.5, w.causal, q_index=idx)
-        flops = 4.0 * H * hd * attn_pairs
-        what = (f"{w.name} core, batch row 0 of {w.batch}: {'causal ' if w.causal else ''}"
-                f"streamed attention of {n_q} query rows x {H} heads over all {S} keys; ")
-    else:
-        params = W.make_params(w)
-        if not w.int8:
-            params = W.round_params(params, w.dtype)
-        pf = {kk: vv.float() for kk, vv in params.items()}
-        x = W.make_input(row, W.TIMING_SEED).float()
-
-        def one():
-            if w.int8:
-                return OI.int8_self_attention(x.to(torch.float16), params, H, w.causal)["out"]
-            if n_q == S:
-                return OA.self_attention(x, pf, H, causal=w.causal)
-            qkv = OA.qkv_projection(x, pf).view(1, S, 3, H, hd)
-            q, k, v = (qkv[:, :, i].transpose(1, 2) for i in range(3))
-            ctx = OS.streamed_attention_core(q[:, :, idx], k, v, hd ** -0.5, w.causal, q_index=idx)
-            ctx = ctx.transpose(1, 2).reshape(1, n_q, d)
-            return torch.nn.functional.linear(ctx, pf["out_proj.weight"], pf["out_proj.bias"])
-        flops = 2.0 * S * d * 3 * d + 4.0 * H * hd * attn_pairs + 2.0 * n_q * d * d
-        what = (f"{w.name} batch row 0 of {w.batch}: QKV projection of all {S} tokens, "
-                f"{'causal ' if w.causal else ''}attention of {n_q} query rows x {H} heads, out "
-                f"projection of those rows; {'int8 recipe (numpy) + ' if w.int8 else ''}")
-    times = []
-    t_all = time.perf_counter()
+    pairs_sample = float((idx + 1).sum() if w.causal else n_q * S)
+    pairs_full = float(B * (S * (S + 1) // 2 if w.causal else S * S))
+    scale = hd ** -0.5
+    stages = {}   # name -> (callable, operations per call, full-workload multiplier)
     with torch.inference_mode():
-        while True:
-            t0 = time.perf_counter_ns()
-            one()
-            times.append((time.perf_counter_ns() - t0) / 1e9)
-            # about budget_s seconds of CPU work, at least 3 calls (bounded for tiny samples)
-            if (time.perf_counter() - t_all > budget_s and len(times) >= 3) or len(times) >= 500:
-                break
-    # the first call carries one-time costs when more than one call fit in the budget
-    timed = times[1:] if len(times) > 1 else times
-    timed.sort()
-    med = timed[len(timed) // 2]
-    unit = "TOP/s" if (w.int8 and not core) else "TFLOP/s"
+        if core:
+            q, k, v = (t.float().permute(0, 2, 1, 3).contiguous()
+                       for t in W.make_core_inputs(row, W.TIMING_SEED))
+            qs = q[:, :, idx].contiguous()
+            stages["attn"] = (lambda: OS.streamed_attention_core(qs, k, v, scale, w.causal,
+                                                                 q_index=idx),
+                              4.0 * H * hd * pairs_sample, pairs_full / pairs_sample)
+            if gpu_eval is not None:
+                ref_rows = stages["attn"][0]()[0].permute(1, 0, 2)           # [n_q, H, hd]
+                got_rows = gpu_eval(*(t.permute(0, 2, 1, 3) for t in (q, k, v)))[0, idx]
+            what = (f"{w.name} core, batch row 0 of {B}: {'causal ' if w.causal else ''}streamed "
+                    f"attention of {n_q} query rows x {H} heads over all {S} keys")
+        else:
+            params = W.make_params(w)
+            if not w.int8:
+                params = W.round_params(params, w.dtype)
+            pf = {kk: vv.float() for kk, vv in params.items()}
+            x = W.make_input(row, W.TIMING_SEED).float()
+            if w.int8:
+                pk = OI.pack_block(params)
+                h = x.to(torch.float16).float().reshape(S, d).numpy()
+                stages["qkv"] = (lambda: OI.int8_linear(h, pk["qkv_w"], pk["qkv_s"], pk["qkv_b"]),
+                                 2.0 * S * d * 3 * d, float(B))
+                qkv = torch.from_numpy(OI.int8_linear(h, pk["qkv_w"], pk["qkv_s"],
+                                                      pk["qkv_b"])[0].astype(np.float16)).float()
+            else:
+                stages["qkv"] = (lambda: OA.qkv_projection(x, pf), 2.0 * S * d * 3 * d, float(B))
+                qkv = OA.qkv_projection(x, pf)
+            q5 = qkv.view(1, S, 3, H, hd)
+            q, k, v = (q5[:, :, i].transpose(1, 2).contiguous() for i in range(3))
+            pd = torch.float16 if w.int8 else None
+            if n_q == S:
+                attn = lambda: OA.attention_core(q, k, v, scale, w.causal, probs_dtype=pd)
+            else:
+                qs = q[:, :, idx].contiguous()
+                attn = lambda: OS.streamed_attention_core(qs, k, v, scale, w.causal, q_index=idx)
+            stages["attn"] = (attn, 4.0 * H * hd * pairs_sample, pairs_full / pairs_sample)
+            ctx = attn().transpose(1, 2).reshape(n_q, d).contiguous()
+            if w.int8:
+                c16 = ctx.to(torch.float16).float().numpy()
+                stages["out"] = (lambda: OI.int8_linear(c16, pk["out_w"], pk["out_s"], pk["out_b"]),
+                                 2.0 * n_q * d * d, T / n_q)
+                ref_out = lambda: torch.from_numpy(stages["out"][0]()[0])
+            else:
+                stages["out"] = (lambda: F.linear(ctx, pf["out_proj.weight"], pf["out_proj.bias"]),
+                                 2.0 * n_q * d * d, T / n_q)
+                ref_out = stages["out"][0]
+            if gpu_eval is not None:
+                ref_rows = ref_out()
+                got_rows = gpu_eval(x)[0, idx]
+            what = (f"{w.name} batch row 0 of {B}: QKV projection of all {S} tokens, "
+                    f"{'causal ' if w.causal else ''}attention of {n_q} query rows x {H} heads, out "
+                    f"projection of those rows{' (int8 recipe in numpy)' if w.int8 else ''}")
+        unit = "TOP/s" if (w.int8 and not core) else "TFLOP/s"
+        report, total_ms = {}, 0.0
+        for name, (fn, ops_, mult) in stages.items():
+            med, n_t, n_all = _time_calls(fn, budget_s / len(stages))
+            report[name] = {"ms_per_call": round(med * 1e3, 3), "ops_per_call": ops_,
+                            "rate": round(ops_ / med / 1e12, 4), "calls_timed": n_t,
+                            "full_workload_multiplier": round(mult, 3),
+                            "ms_full_workload": round(med * mult * 1e3, 1)}
+            total_ms += med * mult * 1e3
+    fl = dict(w.flops())
+    total_ops = fl["attn"] if core else fl["qkv"] + fl["attn"] + fl["out"]
+    extrapolated = any(m > 1.0 for _fn, _o, m in stages.values())
+    parity = None
+    if gpu_eval is not None:
+        from oracle.predicate import compare_outputs
+        r = compare_outputs(ref_rows, got_rows)
+        parity = {"against": ("the int8 recipe (k008_int8_gemm.py:148-225) on CPU" if w.int8 and not core
+                              else "the torch-CPU fp32 oracle"),
+                  "sample": f"batch row 0: {n_q} query rows" + ("" if n_q == S else " spread over the sequence"),
+                  "elements": r.total_elements, "failed": r.failed_elements,
+                  "pass_fraction": round(1.0 - r.failed_elements / max(r.total_elements, 1), 6),
+                  "passed": r.passed, "max_abs_error": r.max_abs_error,
+                  "predicate": "finite and (|d| <= 2e-3 or |d| <= 2e-2 |ref|) elementwise "
+                               "(torch_transformer_benchmark.py:306-316)"}
     return {
-        "value": flops / med / 1e12,
+        "parity": parity,
+        "value": total_ops / (total_ms / 1e3) / 1e12,
         "unit": unit,
         "cores": torch.get_num_threads(),
         "kind": "port",
-        "sample": (f"{what}torch-CPU fp32 oracle; median of {len(timed)} of {len(times)} calls "
-                   f"(time.perf_counter_ns per call), {med * 1e3:.1f} ms/call, "
-                   f"{flops / 1e9:.1f} G{'OP' if unit == 'TOP/s' else 'FLOP'}/call"),
+        "ms_per_iter_extrapolated" if extrapolated else "ms_per_iter": round(total_ms, 2),
+        "stages": report,
+        "sample": (f"{what}; torch-CPU fp32 oracle, each stage timed on its own "
+                   "(time.perf_counter_ns per call, median); the full workload composed from "
+                   "the stage times scaled by their multipliers"
+                   + (" (extrapolated)" if extrapolated else "")),
         "host": hc,
     }
 
@@ -403,6 +491,12 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         samples = sorted(fev[k][0].elapsed_time(fev[k][1]) for k in range(steps))
     else:
         samples = sorted(events[k]["start"].elapsed_time(events[k]["end"]) for k in range(steps))
+    # the events against the host's clock over the same timed rounds (the reference's harness
+    # cross-checks its event timing against wall time, candidate_worker.py:423-429): the ratio
+    # of the larger to the smaller per-step time; above 1.25 the line is flagged
+    wall_ms = wall * 1e3 / steps
+    ev_ms = sum(samples) / steps
+    agreement = max(wall_ms, ev_ms) / max(min(wall_ms, ev_ms), 1e-12)
     ms_step = samples[len(samples) // 2] if steps % 2 else 0.5 * (samples[steps // 2 - 1] + samples[steps // 2])
     timing = {"median_ms": round(ms_step, 5), "mean_ms": round(sum(samples) / steps, 5),
               "p90_ms": round(samples[min(steps - 1, int(0.9 * steps))], 5),
@@ -492,7 +586,23 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
     mode = "core" if core else ("full" if full else ("half" if half else "block"))
     kernel_name = {"qkv": "gemm (QKV projection)", "attn": "attn_fwd", "out": "gemm (out projection)",
                    "ffn_in": "gemm (ffn_in + GELU)", "ffn_out": "gemm (ffn_out + residual)"}[dom]
+    # the GPU path on a CPU-made input (the CPU baseline's sample), for the parity leg
+    if core:
+        def gpu_eval(q_, k_, v_):
+            with torch.inference_mode():
+                o = ops.attention(*(t.to(device=dev, dtype=w.dtype).contiguous() for t in (q_, k_, v_)),
+                                  causal=w.causal)
+            return o.float().cpu()
+    elif not (half or full):
+        def gpu_eval(x_):
+            with torch.inference_mode():
+                xg = x_.to(device=dev, dtype=w.dtype)
+                o = mod.run(xg, torch.ones(xg.shape[:2], dtype=torch.bool, device=dev), w.causal)
+            return o.float().cpu()
+    else:
+        gpu_eval = None
     result = {
+        "_gpu_eval": gpu_eval,
         "metric": "attention-block ms/iter + TFLOP/s (% of MFMA peak) per config, 1 MI355X",
         "value": round(total_ops / ms_step / 1e9, 3),
         "unit": "TOP/s (int8 GEMMs + fp16 SDPA)" if (w.int8 and not core) else "TFLOP/s",
@@ -521,10 +631,17 @@ def measure(name: str, steps: int, warmup: int, min_warmup_s: float = 0.5,
         "roofline": {"kernel": kernel_name, "bound": "mfma", "achieved": round(achieved, 2),
                      "peak": peak, "unit": "TOP/s" if kdt == "int8" else "TFLOP/s",
                      "frac": round(achieved / peak, 4),
-                     "traffic": measured_traffic(name + (":core" if core else ""), dom),
+                     "traffic": measured_traffic(
+                         name + (":core" if core else ""), dom,
+                         stage_kernels(w, dom, torch.float16 if w.int8 else
+                                       (w.dtype if core else
+                                        SelfAttention(w.d_model, w.heads).core_dtype(w.dtype)))),
                      "algorithmic_bytes": by[dom], "dtype": kdt},
         "stages": stage_report,
         "wall_s": round(wall, 3),
+        "event_wall_agreement": {"wall_ms_per_step": round(wall_ms, 5),
+                                 "event_ms_per_step_mean": round(ev_ms, 5),
+                                 "ratio": round(agreement, 4), "flagged": agreement > 1.25},
         "launch": ("graph replay" if graph else
                    ("module forward: replay of its captured graph (launch-bound shape); "
                     "per-stage times from eager steps" if fwd_graph else "eager")),
@@ -695,9 +812,18 @@ def main() -> int:
                                                   and not W.CONFIGS[name].int8) else "own row kernels")
         log(f"[bench] {token}: {res['ms_per_step']} ms/step (median), {res['value']} {res['unit']}, "
             f"roofline {res['roofline']['kernel']} {res['roofline']['frac']}")
-        if not args.no_cpu_baseline:
+        gpu_eval = res.pop("_gpu_eval")
+        if not args.no_cpu_baseline and mode in ("block", "core"):
             log(f"[bench] {token}: cpu baseline (budget {args.cpu_budget}s)")
-            res["cpu_baseline"] = cpu_baseline(W.CONFIGS[name], args.cpu_budget, core=mode == "core")
+            cb = cpu_baseline(W.CONFIGS[name], args.cpu_budget, core=mode == "core",
+                              gpu_eval=gpu_eval)
+            cpu_ms = cb.get("ms_per_iter_extrapolated", cb.get("ms_per_iter"))
+            cb["gpu_speedup_over_cpu"] = round(cpu_ms / res["ms_per_step"], 1)
+            res["parity"] = cb.pop("parity")
+            res["cpu_baseline"] = cb
+            if res["parity"] is not None:
+                log(f"[bench] {token}: parity pass fraction {res['parity']['pass_fraction']} "
+                    f"({res['parity']['failed']} of {res['parity']['elements']} elements fail)")
         else:
             res["cpu_baseline"] = None
         print(json.dumps(res), flush=True)

@@ -93,24 +93,29 @@ int mi355_attn_fwd(int dtype, const void* Q, const void* K, const void* V, void*
 /*
  * mi355_attn_fwd with a caller-provided workspace (same interface and results contract; replaces
  * the same reference code). On the matrix-core kernel (F16 / BF16, head_dim 32, 64, 128) a
- * workspace of at least B * H * ceil(S_k / 1024) * 4 bytes (4-byte aligned) holds the key-norm
- * bounds max |k| per 1024-key chunk of every head, computed by a pass over K on the same stream
- * before the attention launch. A wave whose every query satisfies |c q| max|k| - mu <= 8 (c =
- * scale * log2 e, mu its lazily moved running maximum) can never move mu again, so it skips the
- * per-tile row maxima for the rest of its sweep: the output is bit-identical to mi355_attn_fwd.
- * Calls without a key mask (causal ones over the keys before each 256-query work-group's first
- * query): a wave whose bound keeps every score within +-8 (log2 units) from the start runs with
- * mu = 0 and no row maxima at all (the max-free sweep); its
- * output then differs from mi355_attn_fwd only in rounding, under the same error bound. When
- * the workspace also holds the redo flags (from the next 256-byte boundary after the bounds,
- * one int per 256-query work-group: mi355_attn_workspace_bytes), a wave whose bounds exceed 8
- * may instead fix mu at bound - 8 in advance (the offset sweep); a work-group in which a row's
- * probability sum then stays below 1 is recomputed on the exact path by a second launch on the
- * same stream. Same error bound.
+ * workspace of at least B * H * ceil(S_k / 256) * 4 bytes (4-byte aligned) holds the key-norm
+ * bounds max |k| per 256-key chunk of every head (a chunk is one 256-query work-group tile),
+ * computed by a pass over K on the same stream before the attention launch. A wave whose every
+ * query satisfies |c q| max|k| - mu <= 8 (c = scale * log2 e, mu its lazily moved running
+ * maximum) can never move mu again, so it skips the per-tile row maxima for the rest of its
+ * sweep: the output is bit-identical to mi355_attn_fwd. Causal work-groups reduce only the
+ * chunks of the keys they visit (up to the end of their query tile), so no output row depends
+ * on a key or query past the end of its 256-row tile. On work-groups whose keys are all valid: a
+ * wave whose bound keeps every score within +-8 (log2 units) from the start runs with mu = 0 and
+ * no row maxima at all (the max-free sweep; causal calls over the keys before the work-group's
+ * first query); its output then differs from mi355_attn_fwd only in rounding, under the same
+ * error bound. When the workspace also holds the redo flags (from the next 256-byte boundary
+ * after the bounds, one int per 256-query work-group: mi355_attn_workspace_bytes), a wave whose
+ * bounds exceed 8 may instead fix mu at bound - 8 in advance (the offset sweep); a work-group in
+ * which a row's probability sum then stays below 1 is recomputed on the exact path by a second
+ * launch on the same stream. Same error bound. With a key mask and room for the redo flags, the
+ * bound pass also marks the chunks holding an invalid key; work-groups that visit one leave the
+ * first launch at once and are run by the second launch with the key mask applied (decided on
+ * the device: an all-true mask costs the same as no mask, and nothing waits for the host).
  * workspace may be NULL (then the same as mi355_attn_fwd); a smaller non-NULL workspace than
- * the bounds need is MI355_E_BAD_SIZE. Causal calls with a key mask do not use it. The workspace
- * is scratch: its contents on return are unspecified, and calls that share one workspace must
- * be stream-ordered.
+ * the bounds need is MI355_E_BAD_SIZE. Causal calls with a key mask use it only with room for
+ * the redo flags. The workspace is scratch: its contents on return are unspecified, and calls
+ * that share one workspace must be stream-ordered.
  */
 int mi355_attn_fwd_ws(int dtype, const void* Q, const void* K, const void* V, void* O, int64_t B,
                       int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim,
@@ -127,6 +132,14 @@ int mi355_attn_fwd_ws(int dtype, const void* Q, const void* K, const void* V, vo
  */
 int64_t mi355_attn_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t S_q, int64_t S_k,
                                    int64_t head_dim);
+
+/*
+ * The same workspace size at any key length (bounds and redo flags), for callers that want the
+ * bound pass and the sweeps below the recommended length; 0 when the problem does not run on
+ * the matrix-core kernel. Replaces the same reference code as mi355_attn_fwd.
+ */
+int64_t mi355_attn_workspace_bytes_forced(int dtype, int64_t B, int64_t H, int64_t S_q,
+                                          int64_t S_k, int64_t head_dim);
 
 /*
  * Per-row symmetric int8 quantisation of X[M,K] (row stride ldx) into Xq[M,K] (contiguous) and

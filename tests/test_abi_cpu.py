@@ -128,10 +128,10 @@ def test_attention_argument_validation():
 
 def test_attention_workspace_argument_validation():
     """mi355_attn_fwd_ws: the recommended size is the key-norm bound array of the matrix-core
-    kernel (B * H * ceil(S_k / 1024) floats), rounded up to 256 bytes, then one int per
+    kernel (B * H * ceil(S_k / 256) floats), rounded up to 256 bytes, then one int per
     work-group of 256 queries (the offset sweep's redo flags), from S_k = 32768 on, 0
-    elsewhere; a non-NULL workspace below the bound size or misaligned is refused before any
-    launch."""
+    elsewhere (mi355_attn_workspace_bytes_forced: the same size at any key length); a non-NULL
+    workspace below the bound size or misaligned is refused before any launch."""
     L = _lib()
     h = L.lib()
     codes = _status_codes()
@@ -139,14 +139,20 @@ def test_attention_workspace_argument_validation():
     B, H = 2, 4
 
     def size(S_q, S_k):
-        return (B * H * -(-S_k // 1024) * 4 + 255) // 256 * 256 + B * H * -(-S_q // 256) * 4
-    assert h.mi355_attn_workspace_bytes(1, B, H, 32768, 32768, 64) == size(32768, 32768) == 5120
-    assert h.mi355_attn_workspace_bytes(2, B, H, 10, 100000, 128) == size(10, 100000) == 3360
-    assert h.mi355_attn_workspace_bytes(1, B, H, 40000, 40000, 32) == size(40000, 40000) == 6304
+        return (B * H * -(-S_k // 256) * 4 + 255) // 256 * 256 + B * H * -(-S_q // 256) * 4
+    assert h.mi355_attn_workspace_bytes(1, B, H, 32768, 32768, 64) == size(32768, 32768) == 8192
+    assert h.mi355_attn_workspace_bytes(2, B, H, 10, 100000, 128) == size(10, 100000) == 12576
+    assert h.mi355_attn_workspace_bytes(1, B, H, 40000, 40000, 32) == size(40000, 40000) == 10144
     assert h.mi355_attn_workspace_bytes(1, B, H, 8192, 8192, 64) == 0      # short key range
     assert h.mi355_attn_workspace_bytes(0, B, H, 8192, 8192, 64) == 0      # fp32: VALU kernel
     assert h.mi355_attn_workspace_bytes(1, B, H, 8192, 8192, 80) == 0      # head_dim 80: VALU
-    S = 3000  # 3 chunks
+    # the forced size: the same layout at any key length, 0 off the matrix-core kernel
+    assert h.mi355_attn_workspace_bytes_forced(1, B, H, 8192, 8192, 64) == size(8192, 8192) == 2048
+    assert h.mi355_attn_workspace_bytes_forced(1, B, H, 100, 300, 128) == size(100, 300) == 288
+    assert h.mi355_attn_workspace_bytes_forced(0, B, H, 8192, 8192, 64) == 0
+    assert h.mi355_attn_workspace_bytes_forced(1, B, H, 8192, 8192, 80) == 0
+    assert h.mi355_attn_workspace_bytes_forced(1, B, H, 8192, 0, 64) == 0
+    S = 3000  # 12 chunks
     st = L.i64_array((3 * 64 * H * S, 3 * 64 * H, 64))
     ost = L.i64_array((64 * H * S, 64 * H, 64))
 
@@ -154,7 +160,7 @@ def test_attention_workspace_argument_validation():
         return h.mi355_attn_fwd_ws(1, fake, fake, fake, fake, B, H, S, S, 64, st, st, st, ost,
                                    0.125, 0, None, 0, ws, nbytes, None)
 
-    need = B * H * 3 * 4
+    need = B * H * 12 * 4
     assert call(fake, need - 4) == codes["MI355_E_BAD_SIZE"]
     assert call(fake + 2, need) == codes["MI355_E_ALIGNMENT"]
     # argument validation still precedes the workspace check
@@ -236,3 +242,16 @@ def test_layernorm_cvt_argument_validation():
     assert cvt(0, 1, fake, 32, None, None, 1e-5, fake, 64, 4, 64, None) == codes["MI355_E_BAD_SIZE"]
     assert cvt(0, 1, fake, 8192, None, None, 1e-5, fake, 8192, 4, 8192, None) == codes["MI355_E_UNSUPPORTED"]
     assert cvt(0, 1, fake, 64, None, None, 1e-5, fake, 64, 0, 64, None) == 0
+
+
+def test_noalloc_rejects_rows_beyond_the_array():
+    """mi355_layernorm_gemm_bias_noalloc checks M against its file-scope array (2^20 rows,
+    MI355_NOALLOC_MAX_ROWS) on the host, before any device call: with aligned pointers that are
+    never dereferenced, M = 2^20 + 1 is the size error and nothing is launched."""
+    L = _lib()
+    h = L.lib()
+    codes = _status_codes()
+    fake = 1 << 20                                   # aligned, never dereferenced
+    rc = h.mi355_layernorm_gemm_bias_noalloc(1, 1, fake, 64, fake, 64, fake, fake, 1e-5, fake, 32,
+                                             (1 << 20) + 1, 32, 64, 0, None)
+    assert rc == codes["MI355_E_BAD_SIZE"]

@@ -76,6 +76,45 @@ def test_forward_sees_in_place_updates_and_new_tensors(gpu):
             assert torch.equal(mod(z, mask), mod.run(z, mask))
 
 
+def test_forward_sees_switch_changes(gpu):
+    """A graph captured with one set of module switches is recorded again when one changes: an
+    fp32 model's core dtype switched to fp32 (the vector-ALU attention instead of the fp16
+    matrix-core one) after capture gives the eager fp32-core bits, and the switch back the
+    fp16-core bits again; the same for a transformer's LayerNorm eps."""
+    from tiktok_techjam_2026_track3_amd import Transformer
+    dtype = torch.float32
+    mod = _attn(gpu, dtype)
+    x = _x(gpu, dtype)
+    with torch.inference_mode():
+        half_core = mod.run(x)
+        for _ in range(3):
+            assert torch.equal(mod(x), half_core)
+        assert _captured(mod) == 1
+        mod.fp32_core_dtype = torch.float32
+        full_core = mod.run(x)
+        assert not torch.equal(full_core, half_core)
+        for _ in range(3):
+            assert torch.equal(mod(x), full_core)
+        del mod.fp32_core_dtype                       # back to the class default
+        for _ in range(3):
+            assert torch.equal(mod(x), half_core)
+    cfg = OM.TransformerConfig(batch_size=1, seq_len=64, d_model=128, num_heads=4, ffn_dim=256,
+                               num_layers=2, causal=True)
+    torch.manual_seed(5)
+    model = Transformer(cfg).to(device=gpu, dtype=torch.float16).eval()
+    y = _x(gpu, torch.float16, S=64, d=128, seed=3)
+    with torch.inference_mode():
+        for _ in range(3):
+            a = model(y)
+        model.layers[1].norm2.eps = 0.5
+        model.auto_graph = False
+        want = model(y)
+        model.auto_graph = True
+        assert not torch.equal(a, want)
+        for _ in range(3):
+            assert torch.equal(model(y), want)
+
+
 def test_forward_outputs_are_owned_by_the_caller(gpu):
     dtype = torch.float16
     mod = _attn(gpu, dtype)

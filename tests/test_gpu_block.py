@@ -27,10 +27,12 @@ import int8_requant
 # per element). Measured 0.952-0.957 over seven seeds at the reduced shape (B1 S256 d4096):
 # about 1% of the requantised context codes move by one step (a context value one fp16 ulp from
 # the recipe's, next to a rounding boundary), every row has some, and each moved code shifts its
-# row's outputs by up to s_ctx*|w|*s_w. The floor sits below that spread, as a guard against a
-# context that drifts further from the recipe's; the full-size sampled rows and the golden case
-# measure 0.9998-1.0.
-INT8_E2E_PASS_FLOOR = 0.93
+# row's outputs by up to s_ctx*|w|*s_w. The floor sits just under that spread, as a guard
+# against a context that drifts further from the recipe's.
+INT8_E2E_PASS_FLOOR = 0.945
+# the same at the full C4 size (sampled rows) and on the committed golden case, where far fewer
+# codes sit next to a boundary: measured 0.9998 and 1.0
+INT8_E2E_PASS_FLOOR_FULL = 0.999
 
 pytestmark = pytest.mark.gpu
 

@@ -22,7 +22,7 @@ from oracle.predicate import compare_outputs
 from tiktok_techjam_2026_track3_amd import workloads as W
 
 import int8_requant
-from test_gpu_block import INT8_E2E_PASS_FLOOR, SEEDS
+from test_gpu_block import INT8_E2E_PASS_FLOOR_FULL, SEEDS
 
 pytestmark = pytest.mark.gpu
 
@@ -193,4 +193,57 @@ def test_c4_full_stagewise_sampled_rows(gpu):
     frac, stats = int8_requant.check(keep["ctx"].view(T, d)[rows], ctx_rec, pk["out_w"],
                                      pk["out_s"], pk["out_b"], out.reshape(T, d)[rows])
     print("C4 end to end vs the recipe (sampled rows):", stats, flush=True)
-    assert frac >= INT8_E2E_PASS_FLOOR, stats
+    assert frac >= INT8_E2E_PASS_FLOOR_FULL, stats
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_official_shape14_attention_sampled_rows_to_the_end(gpu, dtype):
+    """The attention of official shape 14 (B 32, S 100000, d 1024, 16 heads of 64, causal; the
+    model's nn.Linear initialisation) on its real input size, as the model runs it (all-true
+    mask, the library's default path at this length: key-norm bounds, the max-free and offset
+    sweeps, redo launch). Sampled query rows up to position 99999 of two batch rows are checked
+    stage by stage: the QKV projection against the oracle projection, the context against the
+    chunk-wise oracle (Project/tools/shape14_eval.py:201-236) on the kernel's own rounded q/k/v,
+    and the output against the oracle out projection of that context, by the reference's
+    predicate."""
+    from tiktok_techjam_2026_track3_amd import SelfAttention
+    B, S, d, H = 32, 100000, 1024, 16
+    hd = d // H
+    torch.manual_seed(1414)
+    mod = SelfAttention(d, H)
+    params = {k: v.detach().clone() for k, v in mod.state_dict().items()}
+    mod = mod.to(device=gpu, dtype=dtype)
+    pf = {k: v.to(dtype).float() for k, v in params.items()}
+    print(f"shape 14 attention dtype={dtype}", flush=True)
+    g = torch.Generator(device=gpu).manual_seed(14)
+    x = torch.randn(B, S, d, device=gpu, generator=g).to(dtype)
+    mask = torch.ones(B, S, dtype=torch.bool, device=gpu)
+    keep = {}
+    with torch.inference_mode():
+        out = mod.run(x, mask, True, keep=keep)
+        torch.cuda.synchronize()
+    assert torch.isfinite(out).all()
+    torch.set_num_threads(16)
+    fixed = [0, 255, 256, 2047, 2048, 32767, 32768, 65535, 65536, 99327, 99328, 99840, 99998, 99999]
+    for b in (0, B - 1):
+        g2 = torch.Generator().manual_seed(140 + b)
+        idx = torch.tensor(sorted(set(fixed + torch.randint(0, S, (10,), generator=g2).tolist())))
+        qkv_b = keep["qkv"].view(B, S, 3, H, hd)[b].float().cpu()
+        ref_qkv = OA.qkv_projection(x[b, idx].float().cpu()[None], pf)[0]
+        r = compare_outputs(ref_qkv, qkv_b[idx].reshape(len(idx), 3 * d))
+        print(f"shape 14 batch {b}: qkv rows {r.summary()}", flush=True)
+        assert r.passed, r.summary()
+        q = qkv_b[idx, 0].transpose(0, 1)[None]
+        k = qkv_b[:, 1].transpose(0, 1)[None]
+        v = qkv_b[:, 2].transpose(0, 1)[None]
+        ctx_ref = OS.streamed_attention_core(q, k, v, hd ** -0.5, True, q_index=idx)
+        ctx = keep["ctx"].view(B, S, H, hd)[b, idx].float().cpu()
+        r = compare_outputs(ctx_ref[0].transpose(0, 1), ctx)
+        print(f"shape 14 batch {b}: context rows up to {int(idx.max())}: {r.summary()}",
+              flush=True)
+        assert r.passed, r.summary()
+        y_ref = torch.nn.functional.linear(ctx.reshape(len(idx), d), pf["out_proj.weight"],
+                                           pf["out_proj.bias"])
+        r = compare_outputs(y_ref, out[b, idx].float().cpu())
+        print(f"shape 14 batch {b}: output rows {r.summary()}", flush=True)
+        assert r.passed, r.summary()

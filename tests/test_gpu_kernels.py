@@ -424,12 +424,14 @@ def test_attention_max_free_sweep_packed_and_mixed_heads(gpu):
 @pytest.mark.parametrize("causal", [False, True])
 def test_attention_key_bound_masked_packed(gpu, dtype, causal):
     """Key-masked launches (exact running max, row maxima skipped once mu can no longer move:
-    bit for bit) and causal packed views without a mask (against the oracle)."""
+    bit for bit; key 3 of every row is invalid, so every work-group takes the key-masked
+    instance) and causal packed views without a mask (against the oracle)."""
     B, S = 2, 1300
     g = torch.Generator().manual_seed(9)
     mask = torch.rand(B, S, generator=g) > 0.2
     mask[:, 0] = True
     mask[1] = torch.arange(S) < 900
+    mask[:, 3] = False
     a, b = _bound_pair(gpu, dtype, B, 2, S, 64, causal, 0.125, 47, key_valid=mask)
     assert torch.equal(a, b)
     if causal:
@@ -473,20 +475,22 @@ def test_attention_offset_sweep_against_oracle(gpu, dtype, hd, S, causal):
     _attn_check(gpu, dtype, 2, 3, S, S, hd, causal, seed=49, key_bound=True)
 
 
-def _redo_flags_call(gpu, q, k, v):
+def _redo_flags_call(gpu, q, k, v, causal=False, mask=None):
     """mi355_attn_fwd_ws with a workspace of the caller's (filled with 0x7f bytes); returns the
-    output and the workspace's ints after the 256-byte aligned bounds (the redo flags, one per
-    work-group of 256 queries, then the untouched fill)."""
+    output and the workspace's ints after the 256-byte aligned bounds (one per 256-key chunk of
+    every head: the redo flags, one per work-group of 256 queries, then the untouched fill)."""
     from tiktok_techjam_2026_track3_amd import _lib as L
     B, S, H, hd = q.shape
-    kb = B * H * ((S + 1023) // 1024) * 4
+    kb = B * H * ((S + 255) // 256) * 4
     off = (kb + 255) // 256 * 256
     n_wg = B * H * ((S + 255) // 256)
     ws = torch.full((off + 4 * n_wg + 256,), 0x7F, device=gpu, dtype=torch.uint8)
     out = torch.empty_like(q)
     st = [L.i64_array((t.stride(0), t.stride(1), t.stride(2))) for t in (q, k, v, out)]
     rc = L.lib().mi355_attn_fwd_ws(L.dtype_code(q.dtype), q.data_ptr(), k.data_ptr(), v.data_ptr(),
-                                   out.data_ptr(), B, H, S, S, hd, *st, hd ** -0.5, 0, None, 0,
+                                   out.data_ptr(), B, H, S, S, hd, *st, hd ** -0.5, int(causal),
+                                   None if mask is None else mask.data_ptr(),
+                                   0 if mask is None else mask.stride(0),
                                    ws.data_ptr(), ws.numel(), None)
     L.check("mi355_attn_fwd_ws", rc)
     torch.cuda.synchronize()
@@ -584,6 +588,128 @@ def test_attention_single_invalid_key_is_seen(gpu, dtype, causal, pos):
     mask = torch.ones(B, S, dtype=torch.bool)
     mask[1, pos] = False   # (causal, pos 0: query 0 of row 1 has no valid key, NaN as in the oracle)
     _attn_check(gpu, dtype, B, 2, S, S, 64, causal, key_valid=mask, seed=91)
+
+
+# ---------------------------------------- key mask with the bound workspace (resolved on the device)
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+@pytest.mark.parametrize("scale", [0.125, 1.0])
+def test_attention_mask_resolved_on_device(gpu, dtype, causal, scale):
+    """A key mask with the bound workspace: row 0 all true, row 1 with one invalid key at 1700
+    (S = 3000). Work-groups whose keys are all valid run the unmasked instance (max-free sweep
+    at scale 0.125, offset sweep at 1.0): row 0, and in causal launches row 1's query tiles
+    that end before the invalid key (rows [0, 1536)), have the bits of the call without a mask.
+    The others are run by the key-masked redo launch: the bits of the key-masked call without
+    the workspace (exact running max). The whole output is checked against the oracle too."""
+    ops = _ops()
+    B, S, H, hd = 2, 3000, 2, 64
+    print(f"mask on device dtype={dtype} causal={causal} scale={scale}", flush=True)
+    q = _rand((B, S, H, hd), dtype, 501, scale=scale).to(gpu)
+    k = _rand((B, S, H, hd), dtype, 502, scale=scale).to(gpu)
+    v = _rand((B, S, H, hd), dtype, 503).to(gpu)
+    mask = torch.ones(B, S, dtype=torch.bool)
+    mask[1, 1700] = False
+    m = mask.to(gpu)
+    out = ops.attention(q, k, v, causal=causal, key_valid=m, key_bound=True).cpu()
+    unmasked = ops.attention(q, k, v, causal=causal, key_bound=True).cpu()
+    masked_exact = ops.attention(q, k, v, causal=causal, key_valid=m, key_bound=False).cpu()
+    assert torch.equal(out[0], unmasked[0])
+    split = 1536 if causal else 0
+    assert torch.equal(out[1, :split], unmasked[1, :split])
+    assert torch.equal(out[1, split:], masked_exact[1, split:])
+    _attn_check(gpu, dtype, B, H, S, S, hd, causal, key_valid=mask, seed=501, qscale=scale,
+                kscale=scale, key_bound=True)
+
+
+@pytest.mark.parametrize("causal", [False, True])
+def test_attention_mask_check_redo_flags(gpu, causal):
+    """The redo flags of a masked call with the workspace (Q, K ~ N(0,1)/8: the max-free sweep,
+    whose results are never redone): exactly the work-groups that visit an invalid key are
+    flagged. Row 0 has its only invalid key at 600 (causal: query tiles 2.. visit it), row 1 is
+    all true; B = 2, H = 2, S = 2000 (8 query tiles per head)."""
+    B, S, H, hd = 2, 2000, 2, 64
+    q = _rand((B, S, H, hd), torch.float16, 511, scale=0.125).to(gpu)
+    k = _rand((B, S, H, hd), torch.float16, 512, scale=0.125).to(gpu)
+    v = _rand((B, S, H, hd), torch.float16, 513).to(gpu)
+    mask = torch.ones(B, S, dtype=torch.bool)
+    mask[0, 600] = False
+    out, flags, n_wg = _redo_flags_call(gpu, q, k, v, causal=causal, mask=mask.to(gpu))
+    nt = (S + 255) // 256
+    # the work-group of (b, h, query tile qt): causal grids run the last query tiles first
+    # (linear index ((nt - 1 - qt) * B + b) * H + h); non-causal grids deal (b, h, qt) to the
+    # 8 XCDs (flag order does not matter here: count per batch row)
+    flags = flags[:n_wg]
+    if causal:
+        want = torch.zeros(n_wg, dtype=torch.int32)
+        for qt in range(nt):
+            for b in range(B):
+                for h in range(H):
+                    lin = ((nt - 1 - qt) * B + b) * H + h
+                    want[lin] = int(b == 0 and (qt + 1) * 256 > 600)
+        assert torch.equal(flags, want)
+    else:
+        assert int(flags.sum()) == H * nt              # every work-group of batch row 0
+    ref = OA.attention_core(*(t.cpu().double().transpose(1, 2) for t in (q, k, v)), hd ** -0.5,
+                            causal, mask).transpose(1, 2)
+    assert float((out.double() - ref).abs().max()) < 2e-3
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hd", [32, 64, 128])
+@pytest.mark.parametrize("scale", [0.125, 1.0])
+def test_attention_causal_rows_ignore_later_tokens(gpu, dtype, hd, scale):
+    """Causal calls with the bound workspace (max-free sweep at scale 0.125, offset sweep at
+    1.0): the output of a 256-row query tile depends on no token after the tile. Replacing
+    every query, key and value from token 1000 on leaves rows [0, 768) (the tiles that end at
+    or before token 1000) bit for bit unchanged, and a call on the first 1024 tokens alone gives
+    rows [0, 1024) of a call on all 4096 bit for bit."""
+    ops = _ops()
+    B, S, H = 1, 4096, 2
+    print(f"causal tiles dtype={dtype} hd={hd} scale={scale}", flush=True)
+    q, k, v = (_rand((B, S, H, hd), dtype, 521 + i, scale=scale if i < 2 else 1.0).to(gpu)
+               for i in range(3))
+    full = ops.attention(q, k, v, causal=True, key_bound=True)
+    q2, k2, v2 = (t.clone() for t in (q, k, v))
+    for i, t in enumerate((q2, k2, v2)):
+        t[:, 1000:] = _rand((B, S - 1000, H, hd), dtype, 531 + i, scale=4.0).to(gpu)
+    changed = ops.attention(q2, k2, v2, causal=True, key_bound=True)
+    assert torch.equal(full[:, :768], changed[:, :768])
+    head = ops.attention(*(t[:, :1024].contiguous() for t in (q, k, v)), causal=True,
+                         key_bound=True)
+    assert torch.equal(head, full[:, :1024])
+
+
+@pytest.mark.parametrize("masked", [False, True])
+def test_attention_long_graph_capture_equals_eager(gpu, masked):
+    """A SelfAttention forward at a key length with the bound workspace (S = 40000, the C5
+    block's d_model 512 and 8 heads) captured in a HIP graph: replays equal the eager forward
+    bit for bit, with the all-true mask and with one whose row 1 has an invalid key (eager and
+    captured calls take the same kernels; nothing in the forward reads the mask on the host)."""
+    from tiktok_techjam_2026_track3_amd import SelfAttention
+    torch.manual_seed(77)
+    mod = SelfAttention(512, 8).to(device=gpu, dtype=torch.float16)
+    B, S = 2, 40000
+    x = torch.randn(B, S, 512, device=gpu).half()
+    mask = torch.ones(B, S, dtype=torch.bool, device=gpu)
+    if masked:
+        mask[1, 31000] = False
+    with torch.inference_mode():
+        eager = mod(x, mask)
+        side = torch.cuda.Stream()
+        side.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(side):
+            mod(x, mask)
+        torch.cuda.current_stream().wait_stream(side)
+        g = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(g):
+            out = mod(x, mask)
+        for rep in range(3):
+            out.zero_()
+            torch.cuda.synchronize()
+            g.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out, eager), f"replay {rep}"
+            mod(x[:1], mask[:1])        # eager work between the replays
 
 
 @pytest.mark.parametrize("K", [64, 1024, 4096])

@@ -85,3 +85,63 @@ def test_same_address_fresh_values(gpu, name, batch, seq, masked, graphed):
         if prev is not None:
             assert not torch.equal(out, prev), "same output for fresh input values"
         prev = out.clone()
+
+
+def _class_snapshot(mod):
+    """Identity of every attribute of the official module's classes (methods, class attributes)."""
+    out = {}
+    for cname in ("BaselineSelfAttention", "BaselineTransformerBlock", "BaselineTransformer",
+                  "UserOptimizedTransformer"):
+        cls = getattr(mod, cname)
+        out[cname] = (cls, cls.__mro__, {k: id(v) for k, v in vars(cls).items()})
+    return out
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
+def test_baseline_invariance_probe(gpu, dtype):
+    """The reference harness runs the official baseline on a probe input before any candidate
+    is built and again after the candidate's trials, and requires bit-equal outputs
+    (Project/harness/candidate_worker.py:352-360, 399-401): building candidates through every
+    insertion point (build(otb, config) with each scope, make_user_optimized_transformer, the
+    in-place swaps on a copy) and running them on the GPU must leave the official module's
+    classes, the baseline's parameters and the baseline's output untouched. (The official
+    module here is the oracle restatement, which runs on the CPU.)"""
+    import copy
+    from oracle import model as OM
+    from tiktok_techjam_2026_track3_amd import build, make_user_optimized_transformer
+    from tiktok_techjam_2026_track3_amd.plugin import swap_attention, swap_blocks, swap_model
+    cfg = OM.TransformerConfig(batch_size=2, seq_len=256, d_model=256, num_heads=4, ffn_dim=512,
+                               num_layers=2, causal=True)
+    before = _class_snapshot(OM)
+    torch.manual_seed(991)
+    baseline = OM.BaselineTransformer(cfg).eval()
+    state = {k: v.detach().clone() for k, v in baseline.state_dict().items()}
+    g = torch.Generator().manual_seed(991_827_331)
+    probe_x = torch.randn(2, 256, 256, generator=g)
+    probe_mask = torch.ones(2, 256, dtype=torch.bool)
+    probe_mask[1, 200:] = False
+    with torch.inference_mode():
+        probe_ref = baseline(probe_x, probe_mask).detach().clone()
+    candidates = [build(OM, cfg), build(OM, cfg, fuse_block=True), build(OM, cfg, full_model=True),
+                  make_user_optimized_transformer(OM)(cfg),
+                  make_user_optimized_transformer(OM, full_model=True)(cfg)]
+    for swap in (swap_attention, swap_blocks, swap_model):
+        twin = copy.deepcopy(baseline)
+        swap(twin)
+        candidates.append(twin)
+    x = torch.randn(2, 256, 256, generator=g).to(dtype).to(gpu)
+    m = probe_mask.to(gpu)
+    with torch.inference_mode():
+        for cand in candidates:
+            cand.load_state_dict(baseline.state_dict(), strict=True)
+            cand = cand.to(device=gpu, dtype=dtype).eval()
+            for _ in range(3):
+                y = cand(x, m)
+            assert torch.isfinite(y[m]).all()
+        probe_now = baseline(probe_x, probe_mask)
+    assert torch.equal(probe_now, probe_ref)
+    assert _class_snapshot(OM) == before
+    assert type(baseline) is OM.BaselineTransformer
+    assert all(type(layer.attention) is OM.BaselineSelfAttention for layer in baseline.layers)
+    for k, v in baseline.state_dict().items():
+        assert torch.equal(v, state[k]), k

@@ -273,17 +273,19 @@ def test_official_shapes_fp32_end_to_end(gpu, shape):
 @pytest.mark.parametrize("dtype", [torch.float32, torch.float16])
 def test_official_shape14_full_length_causal_prefix(gpu, dtype):
     """Official shape 14 at its real size (B 32, S 100000, d 1024, 16 heads, 2 layers, the
-    benchmark's float32 default and float16). Every block is causal and per token elsewhere, so
-    output rows [0, P) depend only on input rows [0, P): the first 2048 rows of the full-length
-    run must equal the same model run on the first 2048 tokens alone (bit for bit), and those are
-    judged by the reference's predicate against the fp32 oracle model (fp32; the 16-bit model is
-    checked block by block at this shape below). The prefix property is checked with the exact
-    running max (key_bound False: the sweeps' offsets depend on the bounds of all keys), and
-    the default run (the library's max-free / offset sweeps) against it by the predicate on
-    2 x 16384 rows. Every output is finite, and a batch row run alone gives the same bits as in
-    the full batch. The fp32 model takes fp16 projection operands
-    only from a size on (SelfAttention.fp16_operand_min_elems), which the 2048-token prefix is
-    below: the threshold is pinned to 0 so all three runs take the full-length run's operands."""
+    benchmark's float32 default and float16). Every block is causal and per token elsewhere, and
+    the attention kernel's choices (key-norm bounds, the max-free and offset sweeps, redo
+    flags) for a 256-row query tile depend on no token after the tile, so output rows [0, P)
+    for P a multiple of 256 depend only on input rows [0, P): the first 2048 rows of the
+    full-length run (the library's default path: bound pass and sweeps at this length) must
+    equal the same model run on the first 2048 tokens alone, bit for bit, and those are judged
+    by the reference's predicate against the fp32 oracle model (fp32; the 16-bit model is
+    checked block by block at this shape below). The default run is also compared with the
+    exact running max (key_bound False) by the predicate on 2 x 16384 rows. Every output is
+    finite, and a batch row run alone gives the same bits as in the full batch. The fp32 model
+    takes fp16 projection operands only from a size on (SelfAttention.fp16_operand_min_elems),
+    which the 2048-token prefix is below: the threshold is pinned to 0 so all runs take the
+    full-length run's operands."""
     shape = OFFICIAL_SHAPES[13]
     cfg = _official_cfg(shape, 32, 100000)
     B, S, d, P = cfg.batch_size, cfg.seq_len, cfg.d_model, 2048
@@ -301,14 +303,14 @@ def test_official_shape14_full_length_causal_prefix(gpu, dtype):
         alone = model(x[B - 1:B].contiguous(), mask[B - 1:B].contiguous())
         assert torch.equal(alone[0], out[B - 1])
         del alone
-        # the exact running max (no key-norm bound workspace): the prefix property bit for bit
+        # the prefix property on the default path, bit for bit
+        prefix = model(x[rows, :P].contiguous(), mask[rows, :P].contiguous())
+        assert torch.equal(prefix, out[rows, :P])
+        # the exact running max (no key-norm bound workspace) against the default run
         for blk in model.layers:
             blk.attention.key_bound = False
-        exact = model(x, mask)
-        prefix = model(x[rows, :P].contiguous(), mask[rows, :P].contiguous())
-        assert torch.equal(prefix, exact[rows, :P])
-        # the default full-length run (max-free / offset sweeps at this length) against it
-        r = compare_outputs(exact[rows, :16384].float().cpu(), out[rows, :16384].float().cpu())
+        exact = model(x[rows].contiguous(), mask[rows].contiguous())
+        r = compare_outputs(exact[:, :16384].float().cpu(), out[rows, :16384].float().cpu())
         print("  default vs exact running max, 2 x 16384 rows:", r.summary(), flush=True)
         assert r.passed, r.summary()
     del out, exact
@@ -396,8 +398,8 @@ def test_block_weight_updates_invalidate_ffn_cache(gpu):
 
 # ---------------------------------------------------------------------- int8 (W8A8) block
 # fraction of the whole int8 block's output elements that must pass the predicate against the
-# quantised recipe (fp32 model)
-INT8_BLOCK_PASS_FLOOR = 0.98
+# quantised recipe (fp32 model; measured 0.989-0.992: four requantisation points)
+INT8_BLOCK_PASS_FLOOR = 0.985
 
 
 def _round(a, dtype):

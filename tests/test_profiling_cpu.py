@@ -10,6 +10,8 @@ from tiktok_techjam_2026_track3_amd import profiling as P
 FIELDS = ["Dispatch_Id", "Kernel_Name", "Counter_Name", "Counter_Value", "Start_Timestamp",
           "End_Timestamp"]
 ATTN = "_ZN12_GLOBAL__N_113attn_fwd_mfmaIDF16_Li64ELi4ELi2ELi2ELi2ELb0ELb0ELb0ELb0EEEvNS_8AttnArgsE"
+REDO = "_ZN12_GLOBAL__N_113attn_fwd_mfmaIDF16_Li64ELi4ELi2ELi2ELi2ELb0ELb0ELb0ELb0ELb1EEEvNS_8AttnArgsE"
+BOUND = "_ZN12_GLOBAL__N_114attn_key_boundIDF16_Li64EEEvNS_8AttnArgsEPf"
 COPY = "void at::native::vectorized_elementwise_kernel<4, at::native::neg_kernel_cuda(...)>"
 
 
@@ -76,3 +78,46 @@ def test_traffic_scales_by_the_copy_calibration(tmp_path):
     assert rec["fetch_bytes"] == pytest.approx(300.0 * 1024 * 2)
     assert rec["write_bytes"] == pytest.approx(100.0 * 1024)
     assert rec["bytes_per_launch"] == pytest.approx(300.0 * 1024 * 2 + 100.0 * 1024)
+
+
+def test_traffic_sums_the_stage_kernels_per_call(tmp_path):
+    """A stage of several launches (sweep, redo, bound pass): each kernel's mean per dispatch,
+    summed -- two calls of three launches give the bytes of one call, not the mean of six."""
+    n = 1 << 20
+    _write(tmp_path / "cf", [(1, COPY, "FETCH_SIZE", n / 1024, 0, 1)])
+    _write(tmp_path / "cw", [(1, COPY, "WRITE_SIZE", n / 1024, 0, 1)])
+    _write(tmp_path / "kf", [(2, ATTN, "FETCH_SIZE", 1000.0, 0, 1), (3, REDO, "FETCH_SIZE", 2.0, 0, 1),
+                             (4, BOUND, "FETCH_SIZE", 50.0, 0, 1), (5, ATTN, "FETCH_SIZE", 1200.0, 0, 1),
+                             (6, REDO, "FETCH_SIZE", 4.0, 0, 1), (7, BOUND, "FETCH_SIZE", 50.0, 0, 1)])
+    _write(tmp_path / "kw", [(2, ATTN, "WRITE_SIZE", 100.0, 0, 1), (3, REDO, "WRITE_SIZE", 0.0, 0, 1),
+                             (4, BOUND, "WRITE_SIZE", 1.0, 0, 1)])
+    rec = P.traffic("C5", "attn_fwd_mfma|attn_key_bound", str(tmp_path / "kf"), str(tmp_path / "kw"),
+                    str(tmp_path / "cf"), str(tmp_path / "cw"), float(n))
+    assert rec["stage"] == "attn"
+    assert sorted(rec["kernels"]) == sorted(P.short_name(k) for k in (ATTN, REDO, BOUND))
+    assert P.short_name(BOUND) == "attn_key_bound<f16,64>"
+    assert rec["fetch_bytes"] == pytest.approx((1100.0 + 3.0 + 50.0) * 1024)
+    assert rec["write_bytes"] == pytest.approx((100.0 + 0.0 + 1.0) * 1024)
+
+
+def test_bench_matches_traffic_records_by_kernel_family(tmp_path, monkeypatch):
+    """bench.py attaches a traffic record only when every kernel it summed belongs to the
+    stage's kernel family on this build (the matrix-core attention and its bound pass, or the
+    vector-ALU kernel), never by a name prefix shared between families."""
+    import json
+    import sys
+    sys.path.insert(0, os.path.dirname(os.path.dirname(os.path.abspath(__file__))))
+    import bench
+    f = tmp_path / "traffic.json"
+    f.write_text(json.dumps({
+        "C2": {"stage": "attn", "bytes_per_launch": 5.0,
+               "kernels": {"attn_fwd_mfma<f16,64,4,2,2,2,0,0,0,0,0>": {}, "attn_key_bound<f16,64>": {}}},
+        "C1": {"stage": "attn", "bytes_per_launch": 7.0, "kernels": {"attn_fwd_f32<64>": {}}},
+        "C3": {"stage": "qkv", "bytes_per_launch": 9.0, "kernels": {"gemm_kernel<bf16>": {}}}}))
+    monkeypatch.setattr(bench, "TRAFFIC_FILE", str(f))
+    mfma = ("attn_fwd_mfma", "attn_key_bound")
+    assert bench.measured_traffic("C2", "attn", mfma) == 5.0
+    assert bench.measured_traffic("C2", "attn", ("attn_fwd_valu",)) is None
+    assert bench.measured_traffic("C1", "attn", mfma) is None        # another family's record
+    assert bench.measured_traffic("C3", "attn", mfma) is None        # another stage's record
+    assert bench.measured_traffic("C4", "attn", mfma) is None        # no record

@@ -35,6 +35,7 @@ _SIGNATURES = {
          C.c_float, C.c_int, _P, _I64, _P],
     ),
     "mi355_attn_workspace_bytes": (_I64, [C.c_int, _I64, _I64, _I64, _I64, _I64]),
+    "mi355_attn_workspace_bytes_forced": (_I64, [C.c_int, _I64, _I64, _I64, _I64, _I64]),
     "mi355_attn_fwd_ws": (
         C.c_int,
         [C.c_int, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,

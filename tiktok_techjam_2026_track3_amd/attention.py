@@ -70,16 +70,14 @@ class SelfAttention(nn.Module):
     # plain projection instead
     fold_norm = True
 
+    # the attention kernel's key-norm bound workspace (ops.attention): None = the library's
+    # choice (long key ranges: the max-free and offset sweeps), False = the exact running max
+    key_bound: Optional[bool] = None
     # fp32 models whose core is fp16 (the matrix-core head dims): the block's projections take
     # fp16 operands too -- the LayerNorms compute in fp32 and write fp16, the weights are packed
     # in fp16, accumulation and the residual stream stay fp32 -- as the reference's fast route
     # runs fp32 models on fp16 tiles (Project/submission/dispatcher_region.py:1017-1091);
     # torch.float32 keeps fp32 operands (the LayerNorms then folded into the projections)
-    # key-mask length from which an all-true mask is checked on the host (_resolve_mask)
-    key_mask_check_min_seq = 32768
-    # the attention kernel's key-norm bound workspace (ops.attention): None = the library's
-    # choice (long key ranges: the max-free and offset sweeps), False = the exact running max
-    key_bound: Optional[bool] = None
     fp32_operand_dtype = torch.float16
     # ... from this many input elements on: below it the fp32 path (LayerNorm folded into
     # 128 x 128-tile fp32 projections) is faster than a LayerNorm launch and 256 x 256-tile fp16
@@ -190,12 +188,13 @@ class SelfAttention(nn.Module):
     def _resolve_mask(self, mask: Optional[torch.Tensor], B: int, S: int, device: torch.device):
         """Returns (key_valid [B,S] bool or None, row_valid [B*S] bool or None).
 
-        A given mask goes to the kernels: the attention kernel checks each work-group's mask
-        bytes on the device and masks element-wise only where a tile holds invalid keys, so an
-        all-true mask costs one byte load per key per work-group and no host synchronisation.
-        From ``key_mask_check_min_seq`` keys on (outside graph capture) an all-true mask is
-        recognised on the host instead and the attention runs without a key mask: there the
-        sync is small beside the launch, and only the unmasked kernel has the offset sweep.
+        A given mask goes to the kernels as it is; nothing is decided on the host. The attention
+        kernel checks each work-group's mask bytes on the device and masks element-wise only
+        where a tile holds invalid keys; with the key-norm bound workspace (long key ranges) the
+        bound pass marks the chunks that hold invalid keys, the unmasked kernel (max-free and
+        offset sweeps) runs every work-group whose keys are all valid and a second, key-masked
+        launch runs the rest. An all-true mask therefore costs about what no mask costs, and the
+        forward never synchronises the host (eager and captured calls take the same kernels).
         """
         if mask is None:
             return None, None
@@ -204,9 +203,6 @@ class SelfAttention(nn.Module):
         if mask.device != device:
             raise ValueError("valid_token_mask must be on the input's device")
         m = mask if mask.is_contiguous() else mask.contiguous()
-        if (S >= self.key_mask_check_min_seq and not torch.cuda.is_current_stream_capturing()
-                and bool(m.all())):
-            return None, m.view(B * S)
         return m, m.view(B * S)
 
     # ----------------------------------------------------------------------------- forward
@@ -226,6 +222,10 @@ class SelfAttention(nn.Module):
 
     # launch-bound forwards (small inputs, inference) replay a captured graph (graph.AutoGraph)
     auto_graph = True
+    # attributes the forward reads besides parameters: a captured graph (graph.AutoGraph) is
+    # recorded again when one of them changes
+    graph_switches = ("bf16_core_dtype", "fp32_core_dtype", "fold_norm", "key_bound",
+                      "fp32_operand_dtype", "fp16_operand_min_elems")
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,
                 causal: bool = False) -> torch.Tensor:

@@ -41,23 +41,31 @@ struct AttnArgs {
   int64_t os0, os1, os2;
   int64_t B, H, Sq, Sk;
   float c;    // scale * log2(e)
+  // key mask [B, S_k] (nullable): applied by the key-masked instances; given to the unmasked
+  // instance together with bounds and redo flags, it only hands work-groups with an invalid key
+  // to the key-masked redo launch
   const uint8_t* kv;
   int64_t kv_sb;
   int n_qtiles;
   int o_vec;  // output base and strides keep every output row 16-byte aligned
   // key-norm bounds (nullable; MFMA kernel): kb[(b * H + h) * kb_n + i] = max |k| over key chunk
-  // i of head (b, h), written by attn_key_bound
+  // i of head (b, h), written by attn_key_bound (sign bit set: the chunk holds an invalid key)
   const float* kb;
   int kb_n;
-  // offset-sweep redo flags (nullable; non-causal MFMA launches without a key mask): one int per
-  // work-group (linear block index). The sweep launch writes every flag, 1 when a row of the
-  // work-group's offset sweep failed its check; the redo launch (the kernel's REDO instance)
-  // runs only the flagged work-groups, without the offset sweep.
+  // redo flags (nullable; MFMA launches without a key mask, or with one and bounds): one int per
+  // work-group (linear block index). The first launch writes every flag: 1 when a row of the
+  // work-group's offset sweep failed its check, or when the work-group visits an invalid key;
+  // the redo launch (the kernel's REDO instance; key-masked when the call has a mask) runs only
+  // the flagged work-groups, without the offset sweep.
   int* redo;
 };
 
-// Keys per chunk of the key-norm bound pass.
-constexpr int KB_CHUNK = 1024;
+// Keys per chunk of the key-norm bound pass: the queries of one MFMA work-group, so that a causal
+// work-group reduces the bounds of exactly the keys it visits, [0, end of its query tile) (no
+// bound, offset or sweep choice then depends on a key after the tile).
+constexpr int KB_CHUNK = 256;
+// chunks per work-group of the bound pass
+constexpr int KB_GROUP = 4;
 // 1 = waves whose key-norm bound keeps every score within +-8 (log2 units) run the max-free sweep
 #ifndef MI355_ATTN_MAXFREE
 #define MI355_ATTN_MAXFREE 1
@@ -255,6 +263,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   constexpr bool OFFSET = OFFSET_INSTANCE<PIPE, CAUSAL, KMASK> && !REDO;
+  // the key-mask check of the first launch (unmasked instances that take bounds)
+  constexpr bool KCHECK = !KMASK && !REDO && KB_INSTANCE<PIPE, CAUSAL, KMASK>;
   const int64_t wg_id = blockIdx.x + static_cast<int64_t>(gridDim.x) *
                                          (blockIdx.y + static_cast<int64_t>(gridDim.y) * blockIdx.z);
   // the redo launch runs only the work-groups that the sweep launch flagged
@@ -303,14 +313,43 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   // s*c of query q can exceed |qf_q| kmax (Cauchy-Schwarz on the rounded operands the MFMAs
   // multiply; the fp32 accumulation error, <= 2^-17 of that product, is covered by the margin
   // in qbound).
-  // The query norms |qf| wait in LDS for the rare rescale branch that reads them (held in
-  // registers, or recomputed there, they stay live across the sweep: the loop-invariant code is
-  // hoisted).
   // (not in the causal key-masked instances: at head_dim 64 the bound test takes them past the
   // register budget; the host passes no bounds to them)
   const bool use_kb = KB_INSTANCE<PIPE, CAUSAL, KMASK> && p.kb != nullptr;
-  __shared__ float qn_lds[QG][NT];
   float kmax = 0.f;
+  const int64_t kend0 = CAUSAL ? ((q_wg + BM) < p.Sk ? (q_wg + BM) : p.Sk) : p.Sk;
+  bool kv_skip = false;  // handed to the key-masked redo launch
+  static_assert(BM % KB_CHUNK == 0, "a causal work-group's key range ends on a bound chunk");
+  if (use_kb) {
+    // causal: only the chunks of the keys this work-group visits, [0, kend) (kend ends on a
+    // chunk boundary or at S_k), so that no row's bits depend on a key after its query tile
+    const float* kbp = p.kb + (b * p.H + h) * p.kb_n;
+    const int n_ch = CAUSAL ? static_cast<int>((kend0 + KB_CHUNK - 1) / KB_CHUNK) : p.kb_n;
+    float m = 0.f;
+    uint32_t sgn = 0u;  // a chunk holds an invalid key: its bound has the sign bit set
+    for (int i = lane; i < n_ch; i += 64) {
+      const float x = kbp[i];
+      m = vmax(m, __builtin_fabsf(x));
+      sgn |= __float_as_uint(x);
+    }
+    // Key-mask check of the unmasked instance (launched with the mask pointer, the bound pass
+    // and redo flags): a work-group whose keys include an invalid one sweeps no keys and flags
+    // itself for the redo launch, which runs it with the key-masked instance (every wave reads
+    // the same chunks, so the decision is the work-group's). (An early return here made the
+    // register allocator spill the bf16 instance.)
+    if constexpr (KCHECK) {
+      kv_skip = p.kv != nullptr && __builtin_amdgcn_ballot_w64((sgn >> 31) != 0u) != 0ull;
+      if (kv_skip && tid == 0) p.redo[wg_id] = 1;
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = vmax(m, __shfl_xor(m, off));
+    kmax = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m)));
+  }
+
+  // The query norms |qf| wait in LDS for the rare rescale branch that reads them (held in
+  // registers, or recomputed there, they stay live across the sweep: the loop-invariant code is
+  // hoisted).
+  __shared__ float qn_lds[QG][NT];
   if (use_kb) {
 #pragma unroll
     for (int n = 0; n < QG; ++n) {
@@ -324,17 +363,12 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
         }
       qn_lds[n][tid] = __builtin_sqrtf(pair_sum(ss));
     }
-    const float* kbp = p.kb + (b * p.H + h) * p.kb_n;
-    float m = 0.f;
-    for (int i = lane; i < p.kb_n; i += 64) m = vmax(m, kbp[i]);
-#pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) m = vmax(m, __shfl_xor(m, off));
-    kmax = __int_as_float(__builtin_amdgcn_readfirstlane(__float_as_int(m)));
   }
   // set once every query of the wave has passed the bound test: no row maxima from then on
   bool nomax = false;
 
-  const int64_t kend = CAUSAL ? ((q_wg + BM) < p.Sk ? (q_wg + BM) : p.Sk) : p.Sk;
+  // keys [0, kend) of this work-group's sweep
+  const int64_t kend = kv_skip ? 0 : kend0;
   const int n_kt = static_cast<int>((kend + BN - 1) / BN);   // 64-key sub-tiles
   const int n_st = (n_kt + KT - 1) / KT;                     // LDS stages
 
@@ -878,7 +912,7 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   // path's maximum alone contributes 1), so that no more of a row's probabilities fall below
   // fp16's normal range than on the exact path; a NaN sum fails it too. A failed work-group is
   // flagged for the redo launch, which overwrites its output from the exact path.
-  if constexpr (OFFSET) {
+  if constexpr (OFFSET || KCHECK) {
     if (p.redo != nullptr) {
       bool low = false;
 #pragma unroll
@@ -887,7 +921,8 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
         low = low || (offset_sweep && q_wave + 32 * n + l32 < p.Sq && !(tot >= 1.0f));
       }
       const int bad = __syncthreads_or(low);
-      if (tid == 0) p.redo[wg_id] = bad != 0 ? 1 : 0;
+      // (a work-group the key-mask check skipped, n_kt = 0 while S_k > 0, flagged itself then)
+      if (tid == 0 && n_kt > 0) p.redo[wg_id] = bad != 0 ? 1 : 0;
     }
   }
 
@@ -953,51 +988,75 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   }
 }
 
-// Key-norm bounds for the MFMA kernel: out[(b * H + h) * n_chunks + i] = max |k|_2 (fp32) over
-// the keys of chunk i (KB_CHUNK keys) of head (b, h); NaN / inf propagate (the bound test then
-// fails). HD / 8 lanes per key, one 16-byte load each; every lane of a wave runs every pass so the
-// lane-group sums see active partners.
+// Key-norm bounds for the MFMA kernel: out[(b * H + h) * kb_n + i] = max |k|_2 (fp32) over the
+// keys of chunk i (KB_CHUNK keys) of head (b, h); NaN / inf propagate (the bound test then
+// fails). With a key mask (p.kv), a chunk holding an invalid key is stored with its sign bit set
+// (its magnitude is still the chunk's bound): the attention prologue reduces |bound| and, in the
+// unmasked instance, hands work-groups that visit such a chunk to the key-masked redo launch.
+// One 256-thread work-group per KB_GROUP chunks; HD / 8 lanes per key, one 16-byte load each, up
+// to 8 loads in flight per lane; every lane of a wave runs every pass so the lane-group sums see
+// active partners.
 template <typename T, int HD>
 __global__ __launch_bounds__(256) void attn_key_bound(AttnArgs p, float* __restrict__ out) {
   constexpr int LK = HD / 8;     // lanes per key
   constexpr int KPP = 256 / LK;  // keys per pass
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int64_t i = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
-  const T* __restrict__ Kb = static_cast<const T*>(p.k) + b * p.ks0 + h * p.ks2;
-  const int64_t k0 = i * KB_CHUNK;
-  const int64_t nk = (p.Sk - k0) < KB_CHUNK ? (p.Sk - k0) : KB_CHUNK;
   // UN passes' loads are issued before any is used, so a lane has UN loads in flight
-  constexpr int UN = 8;
-  float m = 0.f;
-  for (int64_t base = 0; base < nk; base += UN * KPP) {
-    u32x4 v[UN];
+  constexpr int UN = KB_CHUNK / KPP < 8 ? KB_CHUNK / KPP : 8;
+  static_assert(KB_CHUNK % (UN * KPP) == 0 && KB_CHUNK == 256, "chunk shape: one mask byte per thread");
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int64_t h = blockIdx.y, b = blockIdx.z;
+  const T* __restrict__ Kb = static_cast<const T*>(p.k) + b * p.ks0 + h * p.ks2;
+  const uint8_t* __restrict__ kvb = p.kv != nullptr ? p.kv + b * p.kv_sb : nullptr;
+  __shared__ float red[KB_GROUP][4];
+  __shared__ int badw[KB_GROUP][4];
+  for (int c = 0; c < KB_GROUP; ++c) {
+    const int64_t ci = static_cast<int64_t>(blockIdx.x) * KB_GROUP + c;
+    if (ci >= p.kb_n) break;  // uniform over the work-group
+    const int64_t k0 = ci * KB_CHUNK;
+    const int64_t nk = (p.Sk - k0) < KB_CHUNK ? (p.Sk - k0) : KB_CHUNK;
+    float m = 0.f;
+    for (int64_t base = 0; base < nk; base += UN * KPP) {
+      u32x4 v[UN];
 #pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      const int64_t kk = base + u * KPP + tid / LK;
-      v[u] = u32x4{0u, 0u, 0u, 0u};
-      if (kk < nk) v[u] = *reinterpret_cast<const u32x4*>(Kb + (k0 + kk) * p.ks1 + (tid % LK) * 8);
-    }
-#pragma unroll
-    for (int u = 0; u < UN; ++u) {
-      const typename Mfma<T>::frag f = __builtin_bit_cast(typename Mfma<T>::frag, v[u]);
-      float ss = 0.f;
-#pragma unroll
-      for (int r = 0; r < 8; ++r) {
-        const float x = to_f32(f[r]);
-        ss = __builtin_fmaf(x, x, ss);
+      for (int u = 0; u < UN; ++u) {
+        const int64_t kk = base + u * KPP + tid / LK;
+        v[u] = u32x4{0u, 0u, 0u, 0u};
+        if (kk < nk) v[u] = *reinterpret_cast<const u32x4*>(Kb + (k0 + kk) * p.ks1 + (tid % LK) * 8);
       }
 #pragma unroll
-      for (int off = LK / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-      m = vmax(m, ss);
+      for (int u = 0; u < UN; ++u) {
+        const typename Mfma<T>::frag f = __builtin_bit_cast(typename Mfma<T>::frag, v[u]);
+        float ss = 0.f;
+#pragma unroll
+        for (int r = 0; r < 8; ++r) {
+          const float x = to_f32(f[r]);
+          ss = __builtin_fmaf(x, x, ss);
+        }
+#pragma unroll
+        for (int off = LK / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+        m = vmax(m, ss);
+      }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) m = vmax(m, __shfl_xor(m, off));
+    // the chunk's mask bytes, one per thread
+    const bool bad = kvb != nullptr && tid < nk && kvb[k0 + tid] == 0;
+    const uint64_t bw = __builtin_amdgcn_ballot_w64(bad);
+    if (lane == 0) {
+      red[c][wave] = m;
+      badw[c][wave] = bw != 0ull;
     }
   }
-#pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) m = vmax(m, __shfl_xor(m, off));
-  __shared__ float red[4];
-  if (lane == 0) red[wave] = m;
   __syncthreads();
-  if (tid == 0)
-    out[(b * p.H + h) * p.kb_n + i] = __builtin_sqrtf(vmax(vmax(red[0], red[1]), vmax(red[2], red[3])));
+  if (tid < KB_GROUP) {
+    const int64_t ci = static_cast<int64_t>(blockIdx.x) * KB_GROUP + tid;
+    if (ci < p.kb_n) {
+      const float v = __builtin_fabsf(__builtin_sqrtf(
+          vmax(vmax(red[tid][0], red[tid][1]), vmax(red[tid][2], red[tid][3]))));
+      const bool bad = (badw[tid][0] | badw[tid][1] | badw[tid][2] | badw[tid][3]) != 0;
+      out[(b * p.H + h) * p.kb_n + ci] = bad ? -v : v;
+    }
+  }
 }
 
 // VALU kernel: every fp32 problem, and 16-bit head dims the MFMA kernel does not take. LQ lanes
@@ -1285,11 +1344,17 @@ void launch_one(const AttnArgs& a, dim3 grid, dim3 block, hipStream_t s) {
 template <typename T, int HD, int NW, int QG>
 int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, float* kb_ws, int* redo, hipStream_t s) {
   AttnArgs a = a0;
-  if (kb_ws && !(causal && kmask)) {
+  // With a key mask, bounds and redo flags, the unmasked instance (max-free and offset sweeps)
+  // runs every work-group whose keys are all valid, decided on the device from the bound pass's
+  // chunk marks, and the key-masked instance redoes the others: no host synchronisation.
+  const bool kcheck = kmask && kb_ws != nullptr && redo != nullptr;
+  if (kb_ws && (!(causal && kmask) || kcheck)) {
     // the key-norm bounds of every head, read by the attention kernel's prologue
     a.kb_n = static_cast<int>((a.Sk + KB_CHUNK - 1) / KB_CHUNK);
-    hipLaunchKernelGGL((attn_key_bound<T, HD>), dim3(a.kb_n, static_cast<unsigned>(a.H),
-                       static_cast<unsigned>(a.B)), dim3(256), 0, s, a, kb_ws);
+    hipLaunchKernelGGL((attn_key_bound<T, HD>),
+                       dim3(static_cast<unsigned>((a.kb_n + KB_GROUP - 1) / KB_GROUP),
+                            static_cast<unsigned>(a.H), static_cast<unsigned>(a.B)),
+                       dim3(256), 0, s, a, kb_ws);
     a.kb = kb_ws;
   }
   constexpr int BM = NW * 32 * QG;
@@ -1300,7 +1365,16 @@ int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, float* kb_ws, int* 
   const bool flat = n * (NW * 64) <= 0xffffffffLL;  // dispatch size is 32-bit
   if (causal && !flat) return MI355_E_BAD_SIZE;
   if (flat) grid = dim3(static_cast<unsigned>(n), 1, 1);
-  if (causal) {
+  if (kcheck) {
+    a.redo = redo;
+    if (causal) {
+      launch_one<T, HD, NW, QG, true, false>(a, grid, block, s);
+      launch_one<T, HD, NW, QG, true, true, true>(a, grid, block, s);
+    } else {
+      launch_one<T, HD, NW, QG, false, false>(a, grid, block, s);
+      launch_one<T, HD, NW, QG, false, true, true>(a, grid, block, s);
+    }
+  } else if (causal) {
     if (kmask) {
       launch_one<T, HD, NW, QG, true, true>(a, grid, block, s);
     } else {
@@ -1519,8 +1593,13 @@ extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const voi
 
 extern "C" int64_t mi355_attn_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t S_q,
                                               int64_t S_k, int64_t head_dim) {
-  if (B <= 0 || H <= 0 || S_q <= 0 || S_k < MI355_ATTN_KB_MIN_SK || !on_mfma_kernel(dtype, head_dim))
-    return 0;
+  if (S_k < MI355_ATTN_KB_MIN_SK) return 0;
+  return mi355_attn_workspace_bytes_forced(dtype, B, H, S_q, S_k, head_dim);
+}
+
+extern "C" int64_t mi355_attn_workspace_bytes_forced(int dtype, int64_t B, int64_t H, int64_t S_q,
+                                                     int64_t S_k, int64_t head_dim) {
+  if (B <= 0 || H <= 0 || S_q <= 0 || S_k <= 0 || !on_mfma_kernel(dtype, head_dim)) return 0;
   return redo_offset(B, H, S_k) + redo_flag_bytes(B, H, S_q, head_dim);
 }
 

@@ -132,6 +132,20 @@ def _derived_caches(module: nn.Module):
             if k.startswith("_mi355_")]
 
 
+def _switch_modules(module: nn.Module):
+    """The submodules whose plain attributes steer the forward: those listing them in
+    ``graph_switches`` (the attention modules' dtype / fold / key-bound switches) and the
+    LayerNorms (eps)."""
+    return [m for m in module.modules()
+            if getattr(type(m), "graph_switches", None) or isinstance(m, nn.LayerNorm)]
+
+
+def _switch_values(mods) -> tuple:
+    """Current values of those attributes (instance or class), in module order."""
+    return tuple((m.eps,) if isinstance(m, nn.LayerNorm)
+                 else tuple(getattr(m, a) for a in type(m).graph_switches) for m in mods)
+
+
 class _Capture:
     """One captured forward: static input buffers, the graph, its output, and what it read."""
 
@@ -154,28 +168,38 @@ class _Capture:
         self.ptrs = [p.data_ptr() for p in self.params]
         self.vers = [p._version for p in self.tracked]
         self.caches = _derived_caches(module)   # held: keeps what the graph reads alive
+        self.switch_mods = _switch_modules(module)
+        self.switches = _switch_values(self.switch_mods)
         self.last = (None, None)                # (weak reference, version) of the inputs copied
 
     def current(self, module: nn.Module) -> bool:
-        """The module still has the parameters, values and derived weights the graph read (the
-        parameter list is walked only when a registration happened somewhere: that walk costs
-        ~7 us for an attention block, ~70 us for a 4-layer model, per call)."""
+        """The module still has the parameters, values, derived weights and switches (dtype,
+        fold and key-bound attributes of its attention modules, LayerNorm eps) the graph was
+        recorded with (the parameter and module lists are walked only when a registration
+        happened somewhere: that walk costs ~7 us for an attention block, ~70 us for a 4-layer
+        model, per call)."""
         if type(module) is not self.cls:
             return False
         if _REGISTRATION_EPOCH[0] != self.epoch:
             now = list(module.parameters())
             if len(now) != len(self.params) or any(a is not b for a, b in zip(now, self.params)):
                 return False
+            mods = _switch_modules(module)
+            if len(mods) != len(self.switch_mods) or any(a is not b for a, b in zip(mods, self.switch_mods)):
+                return False
             self.epoch = _REGISTRATION_EPOCH[0]
         return ([p._version for p in self.tracked] == self.vers
                 and [p.data_ptr() for p in self.params] == self.ptrs
-                and all(m.__dict__.get(k) is v for m, k, v in self.caches))
+                and all(m.__dict__.get(k) is v for m, k, v in self.caches)
+                and _switch_values(self.switch_mods) == self.switches)
 
     def replay(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
         # The copy is skipped when the caller hands back the same tensor objects with unchanged
         # version counters (the benchmark's timing loop passes one x throughout); any in-place
         # torch update of x or the mask (or of a view of them) bumps the counter. Inference
-        # tensors keep no version counter, so they are always copied.
+        # tensors keep no version counter, so they are always copied. Writes that bypass the
+        # counter (through x.data, or by a kernel given x's raw pointer) are not seen: callers
+        # that update inputs that way set the module's auto_graph to False.
         ref, ver = self.last
         tracked = not x.is_inference() and (mask is None or not mask.is_inference())
         key = (x._version, None if mask is None else mask._version) if tracked else None
@@ -200,8 +224,9 @@ class AutoGraph:
     None when the caller should run eagerly: a CPU or large input (more than
     AUTO_GRAPH_MAX_ELEMS elements), autograd enabled, a capture already in progress (the caller's
     own graph then records the eager kernels), the first call of an input signature, or a
-    capture that no longer matches the module (its parameters or derived weights changed: the
-    graph is dropped and the next call captures again). The signature is x's and the mask's
+    capture that no longer matches the module (its parameters, derived weights or switches --
+    the attention modules' ``graph_switches`` attributes, LayerNorm eps -- changed: the graph is
+    dropped and the next call captures again). The signature is x's and the mask's
     shape, dtype, device and strides plus ``extra`` (e.g. the causal flag); up to ``max_graphs``
     signatures keep their graphs. Outputs are fresh tensors (a clone of the graph's output)."""
 

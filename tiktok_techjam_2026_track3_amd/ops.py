@@ -229,7 +229,9 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[t
     ``key_bound`` selects the key-norm bound pass of the matrix-core kernel (a workspace of
     per-chunk max |k| that lets waves skip the per-tile row maxima, and of the offset sweep's
     redo flags): None = the library's choice (``mi355_attn_workspace_bytes``: long key
-    ranges), True = always, False = never.
+    ranges), True = always (``mi355_attn_workspace_bytes_forced``), False = never. With the
+    workspace, a key mask is resolved on the device: work-groups whose keys are all valid run
+    the unmasked sweeps, the others a second, key-masked launch; nothing synchronises the host.
     """
     _on_gpu(q, k, v, out, key_valid)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
@@ -257,10 +259,8 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[t
     code = L.dtype_code(dt)
     if key_bound is None:
         ws_bytes = L.lib().mi355_attn_workspace_bytes(code, B, H, Sq, Sk, D)
-    elif key_bound and dt != torch.float32 and D in (32, 64, 128):
-        # the per-chunk bounds, then (256-byte aligned) the offset sweep's redo flags: one per
-        # work-group of at least 32 queries
-        ws_bytes = (B * H * ((Sk + 1023) // 1024) * 4 + 255) // 256 * 256 + B * H * ((Sq + 31) // 32) * 4
+    elif key_bound:
+        ws_bytes = L.lib().mi355_attn_workspace_bytes_forced(code, B, H, Sq, Sk, D)
     else:
         ws_bytes = 0
     args = (code, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq, Sk, D,

@@ -7,9 +7,10 @@ reports with the commands that produced them):
   (``*_kernel_stats.csv``): calls, average / min / max duration, share of GPU time.
 * ``pmc DIR``     -- per-kernel per-dispatch averages of every counter in a ``--pmc`` run
   (``*_counter_collection.csv``).
-* ``traffic``     -- HBM bytes per launch of one kernel from a ``FETCH_SIZE`` run and a
-  ``WRITE_SIZE`` run, each scaled by the factor that makes the same counter read exactly the
-  known bytes of a plain copy kernel (``bench.py --copy-calibration``), written as JSON.
+* ``traffic``     -- HBM bytes per call of a stage (the per-dispatch means of the kernels
+  matching a pattern, summed) from a ``FETCH_SIZE`` run and a ``WRITE_SIZE`` run, each scaled
+  by the factor that makes the same counter read exactly the known bytes of a plain copy kernel
+  (``bench.py --copy-calibration``), written as JSON.
 * ``util DIR...`` -- per-kernel compute utilisation from one or more ``--pmc`` runs of the same
   command (counters merged by kernel): MFMA busy, MFMA/VALU co-execution, VALU activity, the
   shader clock, and the MFMA operation count, each with the formula it is computed by.
@@ -19,7 +20,7 @@ Usage::
     python -m tiktok_techjam_2026_track3_amd.profiling stats gpurun_out/prof_C2
     python -m tiktok_techjam_2026_track3_amd.profiling pmc gpurun_out/fetch_C2
     python -m tiktok_techjam_2026_track3_amd.profiling util gpurun_out/pmc1_C2 gpurun_out/pmc2_C2
-    python -m tiktok_techjam_2026_track3_amd.profiling traffic --config C2 --kernel attn_fwd_mfma \\
+    python -m tiktok_techjam_2026_track3_amd.profiling traffic --config C2 --kernel 'attn_fwd_mfma|attn_key_bound' \\
         --fetch gpurun_out/fetch_C2 --write gpurun_out/write_C2 \\
         --copy-fetch gpurun_out/fetch_copy --copy-write gpurun_out/write_copy --copy-bytes N
 """
@@ -211,17 +212,36 @@ def print_util(dirs: List[str]) -> None:
               f"{r.get('SQ_INSTS_VALU', 0):11.4g} {r.get('SQ_INSTS_MFMA', 0):10.4g}")
 
 
+def _per_kernel_mean(table: Dict[str, Dict[str, List[float]]], pattern: str, counter: str) -> Dict[str, float]:
+    """Mean per dispatch of ``counter`` for every kernel (short name) matching ``pattern``."""
+    out: Dict[str, List[float]] = defaultdict(list)
+    for name, cs in table.items():
+        if re.search(pattern, name) and cs.get(counter):
+            out[short_name(name)].extend(cs[counter])
+    if not out:
+        raise ValueError(f"no dispatch of a kernel matching {pattern!r} carries {counter}")
+    return {k: _mean(v) for k, v in out.items()}
+
+
 def traffic(config: str, kernel: str, fetch: str, write: str, copy_fetch: str, copy_write: str,
-            copy_bytes: float) -> dict:
-    """HBM bytes per launch of ``kernel``; FETCH_SIZE / WRITE_SIZE are in KiB per dispatch."""
+            copy_bytes: float, stage: str = "attn") -> dict:
+    """HBM bytes per call of a stage whose launches are the kernels matching ``kernel`` (a
+    regular expression: e.g. the attention kernel's sweep and redo instances and its key-norm
+    bound pass): the per-dispatch means of each matching kernel, summed. FETCH_SIZE /
+    WRITE_SIZE are in KiB per dispatch."""
     cf = _mean(_select(counters(copy_fetch), COPY_KERNEL, "FETCH_SIZE")) * 1024.0
     cw = _mean(_select(counters(copy_write), COPY_KERNEL, "WRITE_SIZE")) * 1024.0
     f_fetch, f_write = copy_bytes / cf, copy_bytes / cw
-    kf = _mean(_select(counters(fetch), kernel, "FETCH_SIZE")) * 1024.0
-    kw = _mean(_select(counters(write), kernel, "WRITE_SIZE")) * 1024.0
-    return {"config": config, "kernel": kernel, "fetch_bytes": kf * f_fetch,
-            "write_bytes": kw * f_write, "bytes_per_launch": kf * f_fetch + kw * f_write,
-            "raw_fetch_kib": kf / 1024.0, "raw_write_kib": kw / 1024.0,
+    kf = _per_kernel_mean(counters(fetch), kernel, "FETCH_SIZE")
+    kw = _per_kernel_mean(counters(write), kernel, "WRITE_SIZE")
+    names = sorted(set(kf) | set(kw))
+    per = {n: {"fetch_bytes": kf.get(n, 0.0) * 1024.0 * f_fetch,
+               "write_bytes": kw.get(n, 0.0) * 1024.0 * f_write} for n in names}
+    fb = sum(v["fetch_bytes"] for v in per.values())
+    wb = sum(v["write_bytes"] for v in per.values())
+    return {"config": config, "stage": stage, "kernel": kernel, "kernels": per,
+            "fetch_bytes": fb, "write_bytes": wb, "bytes_per_launch": fb + wb,
+            "raw_fetch_kib": sum(kf.values()), "raw_write_kib": sum(kw.values()),
             "copy_bytes": copy_bytes, "copy_fetch_factor": f_fetch, "copy_write_factor": f_write}
 
 
@@ -236,6 +256,7 @@ def main(argv=None) -> int:
     for a in ("config", "kernel", "fetch", "write", "copy-fetch", "copy-write"):
         t.add_argument("--" + a, required=True)
     t.add_argument("--copy-bytes", type=float, required=True)
+    t.add_argument("--stage", default="attn", help="the bench stage the kernels make up")
     t.add_argument("--json-out", help="merge the record into this JSON file (keyed by config)")
     u = sub.add_parser("util")
     u.add_argument("dirs", nargs="+")
@@ -247,7 +268,8 @@ def main(argv=None) -> int:
     elif a.cmd == "util":
         print_util(a.dirs)
     else:
-        rec = traffic(a.config, a.kernel, a.fetch, a.write, a.copy_fetch, a.copy_write, a.copy_bytes)
+        rec = traffic(a.config, a.kernel, a.fetch, a.write, a.copy_fetch, a.copy_write, a.copy_bytes,
+                      a.stage)
         print(json.dumps(rec, indent=1))
         if a.json_out:
             data = {}
