@@ -658,25 +658,69 @@ def test_attention_mask_check_redo_flags(gpu, causal):
 @pytest.mark.parametrize("hd", [32, 64, 128])
 @pytest.mark.parametrize("scale", [0.125, 1.0])
 def test_attention_causal_rows_ignore_later_tokens(gpu, dtype, hd, scale):
-    """Causal calls with the bound workspace (max-free sweep at scale 0.125, offset sweep at
-    1.0): the output of a 256-row query tile depends on no token after the tile. Replacing
-    every query, key and value from token 1000 on leaves rows [0, 768) (the tiles that end at
-    or before token 1000) bit for bit unchanged, and a call on the first 1024 tokens alone gives
-    rows [0, 1024) of a call on all 4096 bit for bit."""
+    """Causal calls with the bound workspace at a length where work-groups take the sweeps
+    (S = 34816: query tiles whose key range reaches 32768 keys run the max-free sweep at scale
+    0.125 and the offset sweep at 1.0): the output of a 256-row query tile depends on no token
+    after the tile. Replacing every query, key and value from token 34000 on leaves rows
+    [0, 33792) (the tiles that end at or before token 34000) bit for bit unchanged; a call on
+    the first 33792 tokens alone gives those rows bit for bit; and with the library's default
+    workspace choice a 2048-token prefix (no workspace: the exact running max) gives the first
+    2048 rows of the full-length call (workspace) bit for bit, since tiles shorter than 32768
+    keys never take the sweeps."""
     ops = _ops()
-    B, S, H = 1, 4096, 2
+    B, S, H, P, R = 1, 34816, 2, 34000, 33792
     print(f"causal tiles dtype={dtype} hd={hd} scale={scale}", flush=True)
     q, k, v = (_rand((B, S, H, hd), dtype, 521 + i, scale=scale if i < 2 else 1.0).to(gpu)
                for i in range(3))
     full = ops.attention(q, k, v, causal=True, key_bound=True)
     q2, k2, v2 = (t.clone() for t in (q, k, v))
     for i, t in enumerate((q2, k2, v2)):
-        t[:, 1000:] = _rand((B, S - 1000, H, hd), dtype, 531 + i, scale=4.0).to(gpu)
+        t[:, P:] = _rand((B, S - P, H, hd), dtype, 531 + i, scale=4.0).to(gpu)
     changed = ops.attention(q2, k2, v2, causal=True, key_bound=True)
-    assert torch.equal(full[:, :768], changed[:, :768])
-    head = ops.attention(*(t[:, :1024].contiguous() for t in (q, k, v)), causal=True,
-                         key_bound=True)
-    assert torch.equal(head, full[:, :1024])
+    assert torch.equal(full[:, :R], changed[:, :R])
+    head = ops.attention(*(t[:, :R].contiguous() for t in (q, k, v)), causal=True, key_bound=True)
+    assert torch.equal(head, full[:, :R])
+    default_full = ops.attention(q, k, v, causal=True)
+    default_head = ops.attention(*(t[:, :2048].contiguous() for t in (q, k, v)), causal=True)
+    assert torch.equal(default_head, default_full[:, :2048])
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("hd", [32, 64, 128])
+@pytest.mark.parametrize("scale", [0.125, 1.0])
+def test_attention_causal_sweeps_long_against_reference(gpu, dtype, hd, scale):
+    """Causal attention at S = 33280 with the library's default workspace (the last two query
+    tiles' key ranges reach 32768 keys: max-free sweep at scale 0.125, offset sweep at 1.0, the
+    redo launch), sampled rows against an fp64 evaluation of the same rounded inputs, under the
+    error bound of the exact path (module docstring; the fp16 row-sum tree adds its 4
+    roundings)."""
+    ops = _ops()
+    B, S, H = 1, 33280, 2
+    print(f"causal long dtype={dtype} hd={hd} scale={scale}", flush=True)
+    q = _rand((B, S, H, hd), dtype, 541, scale=scale)
+    k = _rand((B, S, H, hd), dtype, 542, scale=scale)
+    v = _rand((B, S, H, hd), dtype, 543)
+    out = ops.attention(q.to(gpu), k.to(gpu), v.to(gpu), causal=True).cpu().double()
+    g = torch.Generator().manual_seed(544)
+    idx = torch.tensor(sorted(set([0, 255, 32511, 32512, 32767, 32768, 33023, 33024, 33279]
+                                  + torch.randint(32512, S, (24,), generator=g).tolist())))
+    tq = q[0, idx].double().transpose(0, 1)                  # [H, n, hd]
+    tk, tv = (t[0].double().transpose(0, 1) for t in (k, v))  # [H, S, hd]
+    c = hd ** -0.5 * 1.4426950408889634
+    s = (tq @ tk.transpose(-2, -1)) * hd ** -0.5              # [H, n, S]
+    s = s.masked_fill(torch.arange(S)[None, None, :] > idx[None, :, None], float("-inf"))
+    p = torch.softmax(s, dim=-1)
+    ref = (p @ tv).transpose(0, 1)                            # [n, H, hd]
+    pav = (p @ tv.abs()).transpose(0, 1)
+    logit2 = float((tq @ tk.transpose(-2, -1)).abs().max()) * c
+    qk_abs = (tq.abs() @ tk.abs().transpose(-2, -1)).amax(dim=-1, keepdim=True).transpose(0, 1)
+    up = UNIT[dtype]
+    rel = 2 * up + 2.0 ** -18 + 2.0 ** -22 * logit2 + 2 * math.log(2) * up * c * qk_abs
+    if dtype == torch.float16 and hd in (32, 64):
+        rel = rel + 4 * UNIT[dtype]
+    bound = rel * pav + UNIT[dtype] * ref.abs() + 1e-7
+    err = (out[0, idx] - ref).abs()
+    assert _report("causal long sampled rows", err, bound) <= 1.0
 
 
 @pytest.mark.parametrize("masked", [False, True])

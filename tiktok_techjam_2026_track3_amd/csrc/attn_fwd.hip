@@ -66,6 +66,18 @@ struct AttnArgs {
 constexpr int KB_CHUNK = 256;
 // chunks per work-group of the bound pass
 constexpr int KB_GROUP = 4;
+// Key sequences at least this long get the key-norm bound pass from mi355_attn_workspace_bytes.
+// The pass reads K once (per head: S_k rows against the S_q x S_k tiles of the attention), and
+// the row maxima it lets waves skip pay only when a whole work-group's queries pass the bound
+// (small score ranges, as in Q, K ~ N(0,1)/sqrt(head_dim): +5-6% at S = 100000, +14% for
+// head_dim 32); on N(0,1) projections few work-groups pass, so shorter sequences (C3, C4: -1 to
+// -4% with the pass) keep the exact path. Causal work-groups apply the same length to their own
+// key range: only those whose keys [0, end of query tile) number at least this many take the
+// max-free / offset sweeps, so whether a row is swept depends on its tile alone, never on the
+// sequence's total length (a prefix run gives the same bits as the full-length run).
+#ifndef MI355_ATTN_KB_MIN_SK
+#define MI355_ATTN_KB_MIN_SK 32768
+#endif
 // 1 = waves whose key-norm bound keeps every score within +-8 (log2 units) run the max-free sweep
 #ifndef MI355_ATTN_MAXFREE
 #define MI355_ATTN_MAXFREE 1
@@ -150,6 +162,11 @@ MI355_DEVINL int swz(int r) {
 // to 2^-11 per level (each probability is <= 2^8, a sub-tile's 32 per lane sum to <= 2^13).
 #ifndef MI355_ATTN_SUM16
 #define MI355_ATTN_SUM16 1
+#endif
+// the max-free / offset sweeps' branch-free stages pipelined in 32-key units (1; fp16 instances
+// with two query groups) or as whole sub-tiles (0)
+#ifndef MI355_ATTN_MFPIPE
+#define MI355_ATTN_MFPIPE 1
 #endif
 // output rows staged through LDS and stored as 16-byte chunks (1) or stored as 8-byte runs (0)
 #ifndef MI355_ATTN_OSTAGE
@@ -838,8 +855,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
       fixable = fixable && qb - thr <= MU_MAX;  // false for NaN / inf bounds
       mu0 = vmax(mu0, qb - thr);
     }
-    const bool all_in = use_kb && !kmask_live && __builtin_amdgcn_ballot_w64(!in_bound) == 0;
-    bool offset = OFFSET && use_kb && !all_in && __builtin_amdgcn_ballot_w64(!fixable) == 0;
+    // (causal: only work-groups whose own key range reaches the recommended length)
+    const bool long_keys = !CAUSAL || kend0 >= MI355_ATTN_KB_MIN_SK;
+    const bool all_in =
+        use_kb && long_keys && !kmask_live && __builtin_amdgcn_ballot_w64(!in_bound) == 0;
+    bool offset = OFFSET && use_kb && long_keys && !all_in && __builtin_amdgcn_ballot_w64(!fixable) == 0;
     if constexpr (OFFSET) {
       if (offset) {
         // Prediction of the check: the row sums of the first sub-tile (in LDS already) at the
@@ -883,10 +903,135 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
           for (int u = 0; u < U; ++u) stage_mf(st + u, u % NSTAGE, (u + NSTAGE - 1) % NSTAGE);
         }
       };
-      if (!offset) {
-        run_mf(std::false_type{});
+      constexpr bool MFP =
+          MI355_ATTN_MFPIPE && !PIPE && !KMASK && NSTAGE == 2 && KT == 2 && QG == 2 && SUM16;
+      if constexpr (MFP) {
+        // Pipelined form of the same sweep (fp16 instances with two query groups and two-sub-tile
+        // stages): keys go in units of 32 (half a sub-tile); the score MFMAs of the next unit are
+        // issued beside the exponentials of this one, and this unit's P.V MFMAs beside its fp16
+        // packing and row sums, so each wave's instruction stream alternates matrix and vector
+        // work instead of running them in separate phases. At a stage's last unit the V fragments
+        // are read into registers before the barrier, so the next stage's first scores (from the
+        // other ring slot) issue right after it, beside that unit's exponentials. The loads, ring
+        // slots and barriers are those of run_mf; the row sums add the same rounded probabilities
+        // in a tree of the same depth (3 packed levels per unit, one across the two units).
+        auto run_mfp = [&](auto off) MI355_LAMBDA_INLINE {
+          f32x16 sA[QG], sB[QG];
+          f16x2 ps[QG];
+          auto score_u = [&](f32x16 (&sc)[QG], const int slot, const int k, const int t) MI355_LAMBDA_INLINE {
+            f32x16 z;
+#pragma unroll
+            for (int i = 0; i < 16; ++i) z[i] = decltype(off)::value ? -mu0 : 0.f;
+            frag kf[KS];
+#pragma unroll
+            for (int s = 0; s < KS; ++s) kf[s] = kfrag(slot, k, t, s);
+#pragma unroll
+            for (int n = 0; n < QG; ++n) {
+              sc[n] = MF::mma(kf[0], qf[n][0], z);
+#pragma unroll
+              for (int s = 1; s < KS; ++s) sc[n] = MF::mma(kf[s], qf[n][s], sc[n]);
+            }
+          };
+          auto exp_u = [&](f32x16 (&sc)[QG]) MI355_LAMBDA_INLINE {
+#pragma unroll
+            for (int n = 0; n < QG; ++n)
+#pragma unroll
+              for (int i = 0; i < 16; ++i) sc[n][i] = fast_exp2(sc[n][i]);
+          };
+          auto vload_u = [&](frag (&vm)[MT][2], const int slot, const int k, const int t) MI355_LAMBDA_INLINE {
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+              for (int hh = 0; hh < 2; ++hh) vm[mt][hh] = vfrag(slot, k, mt, t, hh);
+          };
+          // probabilities (rounded to T), O^T += V^T . P^T, and the unit's row sums
+          auto finish_u = [&](const f32x16 (&sc)[QG], const frag (&vm)[MT][2], const int t) MI355_LAMBDA_INLINE {
+            frag pf[QG][2];
+#pragma unroll
+            for (int n = 0; n < QG; ++n) {
+              float pv[16];
+#pragma unroll
+              for (int i = 0; i < 16; ++i) pv[i] = sc[n][i];
+              pf[n][0] = pack8<T>(pv);
+              pf[n][1] = pack8<T>(pv + 8);
+            }
+#pragma unroll
+            for (int mt = 0; mt < MT; ++mt)
+#pragma unroll
+              for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int n = 0; n < QG; ++n) oacc[n][mt] = MF::mma(vm[mt][hh], pf[n][hh], oacc[n][mt]);
+#pragma unroll
+            for (int n = 0; n < QG; ++n) {
+              f16x2 r[8];
+#pragma unroll
+              for (int hh = 0; hh < 2; ++hh)
+#pragma unroll
+                for (int j = 0; j < 4; ++j) r[4 * hh + j] = f16x2{pf[n][hh][2 * j], pf[n][hh][2 * j + 1]};
+#pragma unroll
+              for (int i = 0; i < 4; ++i) r[i] = r[2 * i] + r[2 * i + 1];
+#pragma unroll
+              for (int i = 0; i < 2; ++i) r[i] = r[2 * i] + r[2 * i + 1];
+              r[0] = r[0] + r[1];
+              if (t == 0) {
+                ps[n] = r[0];
+              } else {
+                const f16x2 q2 = ps[n] + r[0];
+                lsum[n] += static_cast<float>(q2[0]) + static_cast<float>(q2[1]);
+              }
+            }
+          };
+          // one trip: stages stg (ring slot 0) and stg + 1 (slot 1), units u = 0..7 (slot u / 4,
+          // sub-tile k = (u / 2) % 2, half t = u % 2); sA holds the scores of unit 0 on entry and,
+          // with a next trip, those of its unit 0 on exit
+          auto trip = [&](const int stg, auto next) MI355_LAMBDA_INLINE {
+#pragma unroll
+            for (int u = 0; u < 8; ++u) {
+              f32x16 (&cur)[QG] = (u % 2 == 0) ? sA : sB;
+              f32x16 (&nxt)[QG] = (u % 2 == 0) ? sB : sA;
+              const int slot = u / 4, k = (u / 2) % 2, t = u % 2;
+              if (t == 0) issue_loads((stg + slot) * KT + k + (NSTAGE - 1) * KT, 1 - slot, k);
+              frag vm[MT][2];
+              // (sched_barrier: the unit's two phases -- next scores beside the exponentials, then
+              // V fragments, packing, P.V and row sums -- stay apart; without it the compiler
+              // hoists the next unit's V reads and the instances spill)
+              if (u % 4 != 3) {
+                score_u(nxt, slot, ((u + 1) / 2) % 2, (u + 1) % 2);
+                exp_u(cur);
+                __builtin_amdgcn_sched_barrier(0);
+                vload_u(vm, slot, k, t);
+              } else {
+                // the stage's last unit: V into registers, then the barrier (this wave's loads
+                // into the other slot have landed, every wave is done with this slot)
+                vload_u(vm, slot, k, t);
+                __builtin_amdgcn_s_waitcnt(0);
+                __syncthreads();
+                if (u == 3 || decltype(next)::value) score_u(nxt, 1 - slot, 0, 0);
+                exp_u(cur);
+                __builtin_amdgcn_sched_barrier(0);
+              }
+              finish_u(cur, vm, t);
+              __builtin_amdgcn_sched_barrier(0);
+            }
+          };
+          if (st + U - 1 < n_main) {
+            score_u(sA, 0, 0, 0);
+            for (; st + 2 * U - 1 < n_main; st += U) trip(st, std::true_type{});
+            trip(st, std::false_type{});
+            st += U;
+          }
+        };
+        if (!offset) {
+          run_mfp(std::false_type{});
+        } else {
+          run_mfp(std::integral_constant<bool, OFFSET>{});
+        }
       } else {
-        run_mf(std::integral_constant<bool, OFFSET>{});
+        if (!offset) {
+          run_mf(std::false_type{});
+        } else {
+          run_mf(std::integral_constant<bool, OFFSET>{});
+        }
       }
       if (offset) {
 #pragma unroll
@@ -1458,15 +1603,6 @@ bool head_dim_supported(int64_t hd) {
   }
 }
 
-// Key sequences at least this long get the key-norm bound pass from mi355_attn_workspace_bytes.
-// The pass reads K once (per head: S_k rows against the S_q x S_k tiles of the attention), and
-// the row maxima it lets waves skip pay only when a whole work-group's queries pass the bound
-// (small score ranges, as in Q, K ~ N(0,1)/sqrt(head_dim): +5-6% at S = 100000, +14% for
-// head_dim 32); on N(0,1) projections few work-groups pass, so shorter sequences (C3, C4: -1 to
-// -4% with the pass) keep the exact path.
-#ifndef MI355_ATTN_KB_MIN_SK
-#define MI355_ATTN_KB_MIN_SK 32768
-#endif
 
 bool on_mfma_kernel(int dtype, int64_t head_dim) {
   return (dtype == MI355_F16 || dtype == MI355_BF16) &&
