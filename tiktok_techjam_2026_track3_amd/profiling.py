@@ -123,12 +123,27 @@ def _mean(v: List[float]) -> float:
     return sum(v) / len(v)
 
 
-def print_stats(d: str) -> None:
+def stage_sum(rows: List[dict], pattern: str) -> dict:
+    """Per-call time of a stage made of several launches (e.g. the attention's key-norm bound
+    pass, sweep and redo launch): the average durations of the kernels matching ``pattern``,
+    summed (each is launched once per call of the stage)."""
+    hit = [r for r in rows if re.search(pattern, r["name"])]
+    return {"kernels": [short_name(r["name"]) for r in hit],
+            "calls": min((r["calls"] for r in hit), default=0),
+            "avg_us": sum(r["avg_ns"] for r in hit) / 1e3}
+
+
+def print_stats(d: str, groups: List[str] = ()) -> None:
     rows = kernel_stats(d)
     print(f"{'kernel':82s} {'calls':>6s} {'avg_us':>11s} {'min_us':>11s} {'max_us':>11s} {'pct':>6s}")
     for r in rows[:14]:
         print(f"{short_name(r['name']):82s} {r['calls']:6d} {r['avg_ns'] / 1e3:11.2f} "
               f"{r['min_ns'] / 1e3:11.2f} {r['max_ns'] / 1e3:11.2f} {r['pct']:6.1f}")
+    for gspec in groups:
+        name, _, pattern = gspec.partition("=")
+        s = stage_sum(rows, pattern)
+        print(f"stage {name}: {s['avg_us']:.2f} us per call (sum of the averages of "
+              f"{', '.join(s['kernels'])})")
 
 
 def print_pmc(d: str) -> None:
@@ -250,6 +265,8 @@ def main(argv=None) -> int:
     sub = ap.add_subparsers(dest="cmd", required=True)
     s = sub.add_parser("stats")
     s.add_argument("dir")
+    s.add_argument("--stage", action="append", default=[], metavar="NAME=REGEX",
+                   help="also print the per-call time of a stage made of the matching kernels")
     p = sub.add_parser("pmc")
     p.add_argument("dir")
     t = sub.add_parser("traffic")
@@ -262,7 +279,7 @@ def main(argv=None) -> int:
     u.add_argument("dirs", nargs="+")
     a = ap.parse_args(argv)
     if a.cmd == "stats":
-        print_stats(a.dir)
+        print_stats(a.dir, a.stage)
     elif a.cmd == "pmc":
         print_pmc(a.dir)
     elif a.cmd == "util":
