@@ -71,7 +71,8 @@ class SelfAttention(nn.Module):
     fold_norm = True
 
     # the attention kernel's key-norm bound workspace (ops.attention): None = the library's
-    # choice (long key ranges: the max-free and offset sweeps), False = the exact running max
+    # choice (long key ranges: the max-free and offset sweeps), True = at every length,
+    # False = the exact running max
     key_bound: Optional[bool] = None
     # fp32 models whose core is fp16 (the matrix-core head dims): the block's projections take
     # fp16 operands too -- the LayerNorms compute in fp32 and write fp16, the weights are packed
