@@ -101,12 +101,12 @@ int mi355_attn_fwd(int dtype, const void* Q, const void* K, const void* V, void*
  * sweep: the output is bit-identical to mi355_attn_fwd. Causal work-groups reduce only the
  * chunks of the keys they visit (up to the end of their query tile), so no output row depends
  * on a key or query past the end of its 256-row tile. On work-groups whose keys are all valid: a
- * wave whose bound keeps every score within +-8 (log2 units) from the start runs with mu = 0 and
- * no row maxima at all (the max-free sweep; causal calls over the keys before the work-group's
- * first query); its output then differs from mi355_attn_fwd only in rounding, under the same
- * error bound. When the workspace also holds the redo flags (from the next 256-byte boundary
+ * wave whose bound keeps every score within +-T (log2 units; T = 11 non-causal, 8 causal) from
+ * the start runs with mu = 0 and no row maxima at all (the max-free sweep; causal calls over the
+ * keys before the work-group's first query, in query tiles whose key range reaches 32768 keys);
+ * its output then differs from mi355_attn_fwd only in rounding, under the same error bound. When the workspace also holds the redo flags (from the next 256-byte boundary
  * after the bounds, one int per 256-query work-group: mi355_attn_workspace_bytes), a wave whose
- * bounds exceed 8 may instead fix mu at bound - 8 in advance (the offset sweep); a work-group in
+ * bounds exceed T may instead fix mu at bound - T in advance (the offset sweep); a work-group in
  * which a row's probability sum then stays below 1 is recomputed on the exact path by a second
  * launch on the same stream. Same error bound. With a key mask and room for the redo flags, the
  * bound pass also marks the chunks holding an invalid key; work-groups that visit one leave the
@@ -140,6 +140,27 @@ int64_t mi355_attn_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t S_q,
  */
 int64_t mi355_attn_workspace_bytes_forced(int dtype, int64_t B, int64_t H, int64_t S_q,
                                           int64_t S_k, int64_t head_dim);
+
+/*
+ * mi355_attn_fwd_ws with two more controls, for a caller whose QKV projection already wrote the
+ * key-norm bounds (mi355_gemm_bias_kbound / mi355_layernorm_gemm_bias_kbound, same format and
+ * the same bits as the bound pass; replaces the same reference code as mi355_attn_fwd):
+ *   bounds_ready != 0: the workspace's bound section already holds the bounds of this K (and,
+ *     with a key mask, its chunk marks), so no bound pass is launched; the workspace must
+ *     then be given and hold at least the bounds;
+ *   causal_sweep_min_keys: causal work-groups take the max-free / offset sweeps only when their
+ *     key range [0, end of their 256-row query tile) holds at least this many keys (>= 0;
+ *     mi355_attn_fwd_ws uses 32768). Whatever the value, whether a row is swept depends on its
+ *     own query tile only, so a prefix run still gives the full run's rows bit for bit when
+ *     both runs use the same value and both have the workspace.
+ */
+int mi355_attn_fwd_kb(int dtype, const void* Q, const void* K, const void* V, void* O, int64_t B,
+                      int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim,
+                      const int64_t* q_strides, const int64_t* k_strides,
+                      const int64_t* v_strides, const int64_t* o_strides, float scale,
+                      int causal, const uint8_t* key_valid, int64_t key_valid_sb,
+                      void* workspace, int64_t workspace_bytes, int bounds_ready,
+                      int64_t causal_sweep_min_keys, void* stream);
 
 /*
  * Per-row symmetric int8 quantisation of X[M,K] (row stride ldx) into Xq[M,K] (contiguous) and
@@ -285,6 +306,35 @@ int mi355_layernorm_gemm_bias(int in_dtype, int out_dtype, const void* X, int64_
                               const void* W, int64_t ldw, const float* colsum, const float* bias,
                               float eps, float* stats, void* C, int64_t ldc, int64_t M, int64_t N,
                               int64_t K, int epi, void* stream);
+
+/*
+ * Key-norm bounds from the QKV projection's epilogue. mi355_gemm_bias (and
+ * mi355_layernorm_gemm_bias, with epi = 0) of the packed QKV projection
+ * (torch_transformer_benchmark.py:93-95; Project/submission/dispatcher_region.py:1025) that also
+ * writes, for the K block -- output columns [k_col0, k_col0 + n_heads * head_dim) of the M =
+ * B * seq_len token rows -- the key-norm bounds that mi355_attn_fwd_kb reads with bounds_ready:
+ * key_bounds[(b * n_heads + h) * (seq_len / 256) + i] = max |k| over keys 256 i .. 256 i + 255
+ * of head h of batch row b, computed from the rounded outputs in the order of the attention's
+ * bound pass (the same bits), with the sign bit set when key_valid ([B, seq_len] bytes,
+ * nullable) has a 0 among those keys. key_bounds is the bound section of the attention's
+ * workspace (4-byte aligned). Requires 16-bit inputs and outputs, head_dim 32, 64 or 128,
+ * seq_len, k_col0 and n_heads * head_dim multiples of 256, 16-byte aligned output rows, and a
+ * problem that runs on the 256 x 256-tile kernel; otherwise MI355_E_UNSUPPORTED with nothing
+ * launched (the projection part of the LayerNorm-folded form may have run its statistics
+ * pass), and the caller runs the plain projection and lets the attention run its bound pass.
+ */
+int mi355_gemm_bias_kbound(int in_dtype, int out_dtype, const void* A, int64_t lda,
+                           const void* W, int64_t ldw, const float* bias, void* C, int64_t ldc,
+                           int64_t M, int64_t N, int64_t K, float* key_bounds, int64_t k_col0,
+                           int64_t n_heads, int64_t head_dim, int64_t seq_len,
+                           const uint8_t* key_valid, void* stream);
+int mi355_layernorm_gemm_bias_kbound(int in_dtype, int out_dtype, const void* X, int64_t ldx,
+                                     const void* W, int64_t ldw, const float* colsum,
+                                     const float* bias, float eps, float* stats, void* C,
+                                     int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                     float* key_bounds, int64_t k_col0, int64_t n_heads,
+                                     int64_t head_dim, int64_t seq_len,
+                                     const uint8_t* key_valid, void* stream);
 
 /* largest M of mi355_layernorm_gemm_bias_noalloc (its statistics array: 8 MiB per GPU) */
 #define MI355_NOALLOC_MAX_ROWS (1 << 20)

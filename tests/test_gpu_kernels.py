@@ -527,13 +527,14 @@ def test_attention_offset_sweep_redo_flags(gpu, hd):
 @pytest.mark.parametrize("hd", [32, 64, 128])
 def test_attention_offset_sweep_failed_check_is_redone(gpu, hd):
     """A problem built so that the prediction passes and the check fails: every query points
-    along one unit vector u (|q| = sqrt(head_dim)); key 0 has norm L at cosine 0.83 to u, so the
-    first sub-tile's maximum a0 = 0.83 * |cq| * L lies within log2(S / 64) - 1 of mu0 =
-    1.0078 |cq| L + 1/128 - 8, and every other key is tiny (N(0, 0.01^2)), so the row sums come
-    to about 2^(a0 - mu0) < 1. Every work-group is flagged, and the redo launch gives the exact
-    path's bits."""
+    along one unit vector u (|q| = sqrt(head_dim)); key 0 has norm L at cosine `cos` to u, so
+    the first sub-tile's maximum a0 = cos * |cq| * L lies 2 (log2 units) below mu0 =
+    1.0078 |cq| L + 1/128 - T (T = 11, the non-causal sweeps' largest exponent), within
+    log2(S / 64) - 2 of it, and every other key is tiny (N(0, 0.01^2)), so the row sums come to
+    about 2^(a0 - mu0) = 1/4 < 1. Every work-group is flagged, and the redo launch gives the
+    exact path's bits."""
     ops = _ops()
-    B, S, H = 1, 4096, 2
+    B, S, H, T = 1, 4096, 2, 11.0
     c = hd ** -0.5 * 1.4426950408889634
     g = torch.Generator().manual_seed(307)
     u = torch.randn(hd, generator=g)
@@ -542,10 +543,11 @@ def test_attention_offset_sweep_failed_check_is_redone(gpu, hd):
     w = w - (w @ u) * u
     w = w / w.norm()
     qn = hd ** 0.5
-    L = 60.0 / (c * qn)                                    # bound ~ 60.5, mu0 ~ 52.5, a0 ~ 49.8
+    L = 60.0 / (c * qn)                                    # |cq| L = 60: bound ~ 60.5
+    cos = (60.0 * (1 + 1 / 128) + 1 / 128 - T - 2.0) / 60.0   # a0 = mu0 - 2 ~ 47.5
     q = (u * qn).expand(B, S, H, hd).clone().half()
     k = (torch.randn(B, S, H, hd, generator=g) * 0.01)
-    k[:, 0] = L * (0.83 * u + (1 - 0.83 ** 2) ** 0.5 * w)
+    k[:, 0] = L * (cos * u + (1 - cos ** 2) ** 0.5 * w)
     k = k.half()
     v = torch.randn(B, S, H, hd, generator=g).half()
     q, k, v = q.to(gpu), k.to(gpu), v.to(gpu)

@@ -42,6 +42,22 @@ _SIGNATURES = {
          C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64),
          C.c_float, C.c_int, _P, _I64, _P, _I64, _P],
     ),
+    "mi355_attn_fwd_kb": (
+        C.c_int,
+        [C.c_int, _P, _P, _P, _P, _I64, _I64, _I64, _I64, _I64,
+         C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64), C.POINTER(_I64),
+         C.c_float, C.c_int, _P, _I64, _P, _I64, C.c_int, _I64, _P],
+    ),
+    "mi355_gemm_bias_kbound": (
+        C.c_int,
+        [C.c_int, C.c_int, _P, _I64, _P, _I64, _P, _P, _I64, _I64, _I64, _I64,
+         _P, _I64, _I64, _I64, _I64, _P, _P],
+    ),
+    "mi355_layernorm_gemm_bias_kbound": (
+        C.c_int,
+        [C.c_int, C.c_int, _P, _I64, _P, _I64, _P, _P, C.c_float, _P, _P, _I64, _I64, _I64, _I64,
+         _P, _I64, _I64, _I64, _I64, _P, _P],
+    ),
     "mi355_quant_rows_i8": (C.c_int, [C.c_int, _P, _I64, _P, _P, _I64, _I64, C.c_int, _P]),
     "mi355_layernorm": (C.c_int, [C.c_int, _P, _I64, _P, _P, C.c_float, _P, _I64, _I64, _I64, _P]),
     "mi355_layernorm_cvt": (

@@ -71,9 +71,18 @@ class SelfAttention(nn.Module):
     fold_norm = True
 
     # the attention kernel's key-norm bound workspace (ops.attention): None = the library's
-    # choice (long key ranges: the max-free and offset sweeps), True = at every length,
-    # False = the exact running max
+    # choice (long key ranges: the max-free and offset sweeps) and the causal policy below,
+    # True = at every length, False = the exact running max
     key_bound: Optional[bool] = None
+    # causal calls from this many keys on take the key-norm bounds -- written by the QKV
+    # projection's epilogue where its shapes allow (same bits as the attention's bound pass,
+    # which runs otherwise) -- and their query tiles from this key range on take the max-free /
+    # offset sweeps (head_dim 32 / 64; C3, causal S 8192: +7% attention). A prefix run gives
+    # the full run's rows bit for bit as long as both lengths are on the same side of it.
+    causal_sweep_min_keys = 2048
+    # non-causal calls below the library's recommended length take the bounds when the QKV
+    # projection can write them (C2: +3.5% attention, the offset sweep at 2^11)
+    noncausal_projection_bounds = True
     # fp32 models whose core is fp16 (the matrix-core head dims): the block's projections take
     # fp16 operands too -- the LayerNorms compute in fp32 and write fp16, the weights are packed
     # in fp16, accumulation and the residual stream stay fp32 -- as the reference's fast route
@@ -217,6 +226,36 @@ class SelfAttention(nn.Module):
             raise TypeError(f"unsupported dtype {x.dtype}")
         return x.shape[0], x.shape[1]
 
+    def _bound_plan(self, B: int, S: int, core: torch.dtype, causal: bool,
+                    key_valid: Optional[torch.Tensor],
+                    device: torch.device) -> Optional[ops.KeyBoundTarget]:
+        """Where this forward's key-norm bounds go (``key_bound``, ``causal_sweep_min_keys``,
+        ``noncausal_projection_bounds``), or None to leave the choice to ``ops.attention``."""
+        kb, hd = self.key_bound, self.head_dim
+        if kb is False or core not in (torch.float16, torch.bfloat16) or hd not in (32, 64, 128):
+            return None
+        if kb is None:
+            if hd == 128:  # no sweep pays there (the offset sweep's estimate fails)
+                return None
+            if causal and S < self.causal_sweep_min_keys:
+                return None
+            if not causal and not self.noncausal_projection_bounds:
+                return None
+        ws = ops.attention_workspace(B, S, S, self.num_heads, hd, core, device)
+        if ws.numel() == 0:
+            return None
+        return ops.KeyBoundTarget(ws, k_col0=self.d_model, heads=self.num_heads, head_dim=hd,
+                                  seq=S, key_valid=key_valid)
+
+    def _attend(self, q, k, v, causal: bool, key_valid: Optional[torch.Tensor],
+                kbt: Optional[ops.KeyBoundTarget]) -> torch.Tensor:
+        if kbt is not None and (kbt.written or causal or self.key_bound):
+            return ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid,
+                                 workspace=kbt.workspace, bounds_ready=kbt.written,
+                                 causal_sweep_min_keys=self.causal_sweep_min_keys)
+        return ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid,
+                             key_bound=self.key_bound)
+
     def _qkv_views(self, qkv: torch.Tensor, B: int, S: int):
         qkv5 = qkv.view(B, S, 3, self.num_heads, self.head_dim)
         return qkv5[:, :, 0], qkv5[:, :, 1], qkv5[:, :, 2]
@@ -226,6 +265,7 @@ class SelfAttention(nn.Module):
     # attributes the forward reads besides parameters: a captured graph (graph.AutoGraph) is
     # recorded again when one of them changes
     graph_switches = ("bf16_core_dtype", "fp32_core_dtype", "fold_norm", "key_bound",
+                      "causal_sweep_min_keys", "noncausal_projection_bounds",
                       "fp32_operand_dtype", "fp16_operand_min_elems")
 
     def forward(self, x: torch.Tensor, valid_token_mask: Optional[torch.Tensor] = None,
@@ -258,12 +298,12 @@ class SelfAttention(nn.Module):
         x2 = x.reshape(B * S, d)
         if x2.stride(1) != 1:
             x2 = x2.contiguous()
+        kbt = self._bound_plan(B, S, core, causal, key_valid, x.device)
         mark("qkv")
-        qkv = ops.linear(x2, w_qkv, b_qkv, out_dtype=core)
+        qkv = ops.linear(x2, w_qkv, b_qkv, out_dtype=core, key_bounds=kbt)
         q, k, v = self._qkv_views(qkv, B, S)
         mark("attn")
-        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid,
-                                key_bound=self.key_bound)
+        ctx = self._attend(q, k, v, causal, key_valid, kbt)
         mark("out")
         out = ops.linear(ctx.view(B * S, d), w_o, b_o, row_valid=row_valid, out_dtype=x.dtype)
         mark("end")
@@ -305,20 +345,21 @@ class SelfAttention(nn.Module):
         x2 = x.reshape(B * S, d)
         if not x2.is_contiguous():
             x2 = x2.contiguous()
+        kbt = self._bound_plan(B, S, core, causal, key_valid, x.device)
         if self.folds_norm(x.dtype, x.numel()):
             wf, colsum, bf = self._ln_folded_qkv(norm, x.dtype, x.device)
             mark("qkv")
-            qkv = ops.layernorm_linear(x2, wf, colsum, bf, norm.eps, out_dtype=core)
+            qkv = ops.layernorm_linear(x2, wf, colsum, bf, norm.eps, out_dtype=core,
+                                       key_bounds=kbt)
         else:
             mark("norm")
             h = ops.layer_norm(x2, w_n.detach() if w_n is not None else None,
                                b_n.detach() if b_n is not None else None, norm.eps, out_dtype=op)
             mark("qkv")
-            qkv = ops.linear(h, w_qkv, b_qkv, out_dtype=core)
+            qkv = ops.linear(h, w_qkv, b_qkv, out_dtype=core, key_bounds=kbt)
         q, k, v = self._qkv_views(qkv, B, S)
         mark("attn")
-        ctx = ops.attention(q, k, v, scale=self.scale, causal=causal, key_valid=key_valid,
-                                key_bound=self.key_bound)
+        ctx = self._attend(q, k, v, causal, key_valid, kbt)
         mark("out")
         out = ops.linear(ctx.view(B * S, d), w_o, b_o, row_valid=row_valid, out_dtype=x.dtype,
                          residual=x2)

@@ -52,6 +52,9 @@ struct AttnArgs {
   // i of head (b, h), written by attn_key_bound (sign bit set: the chunk holds an invalid key)
   const float* kb;
   int kb_n;
+  // causal work-groups take the max-free / offset sweeps only when their key range [0, end of
+  // query tile) holds at least this many keys
+  int64_t sweep_min_k;
   // redo flags (nullable; MFMA launches without a key mask, or with one and bounds): one int per
   // work-group (linear block index). The first launch writes every flag: 1 when a row of the
   // work-group's offset sweep failed its check, or when the work-group visits an invalid key;
@@ -78,10 +81,25 @@ constexpr int KB_GROUP = 4;
 #ifndef MI355_ATTN_KB_MIN_SK
 #define MI355_ATTN_KB_MIN_SK 32768
 #endif
-// 1 = waves whose key-norm bound keeps every score within +-8 (log2 units) run the max-free sweep
+// 1 = waves whose key-norm bound keeps every score within +-MI355_ATTN_SWEEP_THR (log2 units) run
+// the max-free sweep
 #ifndef MI355_ATTN_MAXFREE
 #define MI355_ATTN_MAXFREE 1
 #endif
+// Largest unnormalised probability of the non-causal max-free and offset sweeps,
+// 2^MI355_ATTN_SWEEP_THR. The exact path keeps 2^8 (its lazy running max); the sweeps may allow
+// more: the fp16 row-sum tree adds at most 16 probabilities before converting to fp32, so
+// 16 * 2^11 = 2^15 stays below fp16's largest finite value, and every rounding involved is
+// relative. A larger value lowers the offset sweep's mu0 = bound - thr, i.e. raises its
+// probabilities, so fewer waves are predicted to fail the row-sum check: at C2's shape on its
+// N(0,1) projections 97% of the waves take the offset sweep at 2^11 against 14% at 2^8 (+3.5%
+// attention with the bounds from the projection). Causal launches keep 2^8: there the waves
+// the larger value admits fail the check more often than they gain (C3 -1% at 2^11).
+#ifndef MI355_ATTN_SWEEP_THR
+#define MI355_ATTN_SWEEP_THR 11
+#endif
+static_assert(MI355_ATTN_SWEEP_THR >= 8 && MI355_ATTN_SWEEP_THR <= 11,
+              "sweep probabilities between 2^8 and 2^11");
 
 // MFMA kernel instances that take key-norm bounds
 template <bool PIPE, bool CAUSAL, bool KMASK>
@@ -158,8 +176,10 @@ MI355_DEVINL int swz(int r) {
 
 // fp16 row sums per sub-tile (head_dim 32 and 64): 1 = a tree of packed fp16 adds over the rounded
 // probabilities (then fp32 across sub-tiles), 0 = fp32 adds of the unrounded ones. The tree is 30 instructions
-// per 64 probabilities against 62 (measured +1.5% at C5, +3% at C3); its partial sums stay exact
-// to 2^-11 per level (each probability is <= 2^8, a sub-tile's 32 per lane sum to <= 2^13).
+// per 64 probabilities against 62 (measured +1.5% at C5, +3% at C3); each partial sum is rounded
+// to 2^-11 of itself per level, and each half of the packed result adds 16 probabilities (each
+// <= 2^8 on the exact path, <= 2^11 in the non-causal sweeps: at most 2^15, below fp16's
+// largest finite value).
 #ifndef MI355_ATTN_SUM16
 #define MI355_ATTN_SUM16 1
 #endif
@@ -837,26 +857,27 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   bool offset_sweep = false;  // this wave runs the offset sweep
   if constexpr (MAXFREE_INSTANCE<PIPE, CAUSAL, KMASK>) {
     // Max-free sweep: when the key-norm bound puts every score of the wave's queries within
-    // [-thr, thr] (|s*c| <= |cq| max|k|), mu stays 0 for the whole sweep: probabilities lie in
-    // [2^-thr, 2^thr] and no row maximum is ever needed.
+    // [-sthr, sthr] (|s*c| <= |cq| max|k|), mu stays 0 for the whole sweep: probabilities lie in
+    // [2^-sthr, 2^sthr] and no row maximum is ever needed.
     // Offset sweep (otherwise; instances without a key mask, first launch, finite bounds up to
-    // thr + MU_MAX): mu is fixed in advance at mu0 = the larger bound - thr of the lane's two
-    // queries, which keeps every probability <= 2^thr as the running max would, with no row
-    // maxima either. Whether the probabilities came out large enough is checked at the end.
+    // sthr + MU_MAX): mu is fixed in advance at mu0 = the larger bound - sthr of the lane's two
+    // queries, which keeps every probability <= 2^sthr, with no row maxima either (the generic
+    // stages after the sweep keep mu0 and skip the maxima too). Whether the probabilities came out large enough is checked at the end.
     // The stages whose sub-tiles are all full and whose look-ahead loads are all in range run
     // as one branch-free basic block (score chains from zero or -mu0, exponentials, P.V), the
     // rest through the generic stage below.
+    constexpr float sthr = CAUSAL ? 8.0f : static_cast<float>(MI355_ATTN_SWEEP_THR);
     bool in_bound = use_kb && !kmask_live, fixable = OFFSET && use_kb && p.redo;
     float mu0 = 0.f;
 #pragma unroll
     for (int n = 0; n < QG; ++n) {
       const float qb = qbound(n);
-      in_bound = in_bound && qb <= thr;
-      fixable = fixable && qb - thr <= MU_MAX;  // false for NaN / inf bounds
-      mu0 = vmax(mu0, qb - thr);
+      in_bound = in_bound && qb <= sthr;
+      fixable = fixable && qb - sthr <= MU_MAX;  // false for NaN / inf bounds
+      mu0 = vmax(mu0, qb - sthr);
     }
-    // (causal: only work-groups whose own key range reaches the recommended length)
-    const bool long_keys = !CAUSAL || kend0 >= MI355_ATTN_KB_MIN_SK;
+    // (causal: only work-groups whose own key range reaches the call's sweep length)
+    const bool long_keys = !CAUSAL || kend0 >= p.sweep_min_k;
     const bool all_in =
         use_kb && long_keys && !kmask_live && __builtin_amdgcn_ballot_w64(!in_bound) == 0;
     bool offset = OFFSET && use_kb && long_keys && !all_in && __builtin_amdgcn_ballot_w64(!fixable) == 0;
@@ -1487,19 +1508,22 @@ void launch_one(const AttnArgs& a, dim3 grid, dim3 block, hipStream_t s) {
 }
 
 template <typename T, int HD, int NW, int QG>
-int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, float* kb_ws, int* redo, hipStream_t s) {
+int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, float* kb_ws, int* redo,
+                bool bounds_ready, hipStream_t s) {
   AttnArgs a = a0;
   // With a key mask, bounds and redo flags, the unmasked instance (max-free and offset sweeps)
   // runs every work-group whose keys are all valid, decided on the device from the bound pass's
   // chunk marks, and the key-masked instance redoes the others: no host synchronisation.
   const bool kcheck = kmask && kb_ws != nullptr && redo != nullptr;
   if (kb_ws && (!(causal && kmask) || kcheck)) {
-    // the key-norm bounds of every head, read by the attention kernel's prologue
+    // the key-norm bounds of every head, read by the attention kernel's prologue (already in
+    // the workspace when a projection epilogue wrote them)
     a.kb_n = static_cast<int>((a.Sk + KB_CHUNK - 1) / KB_CHUNK);
-    hipLaunchKernelGGL((attn_key_bound<T, HD>),
-                       dim3(static_cast<unsigned>((a.kb_n + KB_GROUP - 1) / KB_GROUP),
-                            static_cast<unsigned>(a.H), static_cast<unsigned>(a.B)),
-                       dim3(256), 0, s, a, kb_ws);
+    if (!bounds_ready)
+      hipLaunchKernelGGL((attn_key_bound<T, HD>),
+                         dim3(static_cast<unsigned>((a.kb_n + KB_GROUP - 1) / KB_GROUP),
+                              static_cast<unsigned>(a.H), static_cast<unsigned>(a.B)),
+                         dim3(256), 0, s, a, kb_ws);
     a.kb = kb_ws;
   }
   constexpr int BM = NW * 32 * QG;
@@ -1634,7 +1658,8 @@ int attn_fwd_impl(int dtype, const void* Q, const void* K, const void* V, void* 
                   int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim, const int64_t* q_strides,
                   const int64_t* k_strides, const int64_t* v_strides, const int64_t* o_strides,
                   float scale, int causal, const uint8_t* key_valid, int64_t key_valid_sb,
-                  void* workspace, int64_t workspace_bytes, void* stream) {
+                  void* workspace, int64_t workspace_bytes, bool bounds_ready,
+                  int64_t sweep_min_k, void* stream) {
   if (B < 0 || H < 0 || S_q < 0 || S_k < 0 || head_dim <= 0) return MI355_E_BAD_SIZE;
   if (B == 0 || H == 0 || S_q == 0) return MI355_OK;
   if (!Q || !K || !V || !O || !q_strides || !k_strides || !v_strides || !o_strides)
@@ -1676,6 +1701,7 @@ int attn_fwd_impl(int dtype, const void* Q, const void* K, const void* V, void* 
   a.c = scale * 1.4426950408889634f;
   a.kv = key_valid;
   a.kv_sb = key_valid_sb;
+  a.sweep_min_k = sweep_min_k;
   {
     const int64_t es = dtype == MI355_F32 ? 4 : 2;
     a.o_vec = ((reinterpret_cast<uintptr_t>(O) & 15u) == 0 && (o_strides[0] * es) % 16 == 0 &&
@@ -1691,6 +1717,7 @@ int attn_fwd_impl(int dtype, const void* Q, const void* K, const void* V, void* 
   }
   float* kb = nullptr;
   int* redo = nullptr;
+  if (bounds_ready && workspace == nullptr) return MI355_E_NULL_POINTER;
   if (workspace != nullptr && S_k > 0) {
     if (workspace_bytes < key_bound_bytes(B, H, S_k)) return MI355_E_BAD_SIZE;
     if (reinterpret_cast<uintptr_t>(workspace) & 3u) return MI355_E_ALIGNMENT;
@@ -1702,16 +1729,16 @@ int attn_fwd_impl(int dtype, const void* Q, const void* K, const void* V, void* 
   }
   if (dtype == MI355_F16) {
     if (head_dim == 32)
-      return launch_mfma<_Float16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, kb, redo, s);
+      return launch_mfma<_Float16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, kb, redo, bounds_ready, s);
     return head_dim == 64
-               ? launch_mfma<_Float16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, kb, redo, s)
-               : launch_mfma<_Float16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, kb, redo, s);
+               ? launch_mfma<_Float16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, kb, redo, bounds_ready, s)
+               : launch_mfma<_Float16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, kb, redo, bounds_ready, s);
   }
   if (head_dim == 32)
-    return launch_mfma<__bf16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, kb, redo, s);
+    return launch_mfma<__bf16, 32, MI355_ATTN_NW32, MI355_ATTN_QG32>(a, cz, kmask, kb, redo, bounds_ready, s);
   return head_dim == 64
-             ? launch_mfma<__bf16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, kb, redo, s)
-             : launch_mfma<__bf16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, kb, redo, s);
+             ? launch_mfma<__bf16, 64, MI355_ATTN_NW64, MI355_ATTN_QG64>(a, cz, kmask, kb, redo, bounds_ready, s)
+             : launch_mfma<__bf16, 128, MI355_ATTN_NW128, MI355_ATTN_QG128>(a, cz, kmask, kb, redo, bounds_ready, s);
 }
 
 }  // namespace
@@ -1724,7 +1751,7 @@ extern "C" int mi355_attn_fwd(int dtype, const void* Q, const void* K, const voi
                               void* stream) {
   return attn_fwd_impl(dtype, Q, K, V, O, B, H, S_q, S_k, head_dim, q_strides, k_strides,
                        v_strides, o_strides, scale, causal, key_valid, key_valid_sb, nullptr, 0,
-                       stream);
+                       false, MI355_ATTN_KB_MIN_SK, stream);
 }
 
 extern "C" int64_t mi355_attn_workspace_bytes(int dtype, int64_t B, int64_t H, int64_t S_q,
@@ -1747,5 +1774,18 @@ extern "C" int mi355_attn_fwd_ws(int dtype, const void* Q, const void* K, const 
                                  void* workspace, int64_t workspace_bytes, void* stream) {
   return attn_fwd_impl(dtype, Q, K, V, O, B, H, S_q, S_k, head_dim, q_strides, k_strides,
                        v_strides, o_strides, scale, causal, key_valid, key_valid_sb, workspace,
-                       workspace_bytes, stream);
+                       workspace_bytes, false, MI355_ATTN_KB_MIN_SK, stream);
+}
+
+extern "C" int mi355_attn_fwd_kb(int dtype, const void* Q, const void* K, const void* V, void* O,
+                                 int64_t B, int64_t H, int64_t S_q, int64_t S_k, int64_t head_dim,
+                                 const int64_t* q_strides, const int64_t* k_strides,
+                                 const int64_t* v_strides, const int64_t* o_strides, float scale,
+                                 int causal, const uint8_t* key_valid, int64_t key_valid_sb,
+                                 void* workspace, int64_t workspace_bytes, int bounds_ready,
+                                 int64_t causal_sweep_min_keys, void* stream) {
+  if (causal_sweep_min_keys < 0) return MI355_E_BAD_SIZE;
+  return attn_fwd_impl(dtype, Q, K, V, O, B, H, S_q, S_k, head_dim, q_strides, k_strides,
+                       v_strides, o_strides, scale, causal, key_valid, key_valid_sb, workspace,
+                       workspace_bytes, bounds_ready != 0, causal_sweep_min_keys, stream);
 }

@@ -46,6 +46,16 @@ struct GemmArgs {
   int64_t M, N, K;
   int out_dtype;
   int epi;  // EPI_* flags
+  // Key-norm bounds of the attention that reads this projection's output (nullable; the
+  // 256 x 256-tile instances with 16-bit outputs). The K block is columns [kb_col0, kb_col0 +
+  // kb_heads * kb_hd), rows are kb_seq tokens per batch row: the tile of rows [m0, m0 + 256)
+  // and the head's columns is key chunk (m0 % kb_seq) / 256 of batch row m0 / kb_seq, and its
+  // bound max |k| is stored at kb_out[(b * kb_heads + h) * (kb_seq / 256) + chunk], with the
+  // sign bit set when a row of the chunk has kb_valid 0 (the attention's bound pass format).
+  float* kb_out;
+  const uint8_t* kb_valid;
+  int64_t kb_col0, kb_seq;
+  int kb_hd, kb_heads;
 };
 
 // Epilogue options beyond bias / row mask / residual:
@@ -178,6 +188,9 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
   constexpr int C_PITCH = BN * static_cast<int>(sizeof(TO)) + 16;
   constexpr int STAGE_BYTES = NST * (BM + BN) * CHK * 16;
   constexpr bool STAGE_C = BM * C_PITCH <= 160 * 1024 - 1024;
+  // the key-norm bound epilogue (GemmArgs::kb_out): staged 256 x 256 tiles of 16-bit outputs
+  constexpr bool KB_EPI = STAGE_C && BM == 256 && BN == 256 && sizeof(TO) == 2 && !INT8 &&
+                          !PERSIST && WM * WN == 8;
   constexpr int LDS_BYTES = (STAGE_C && BM * C_PITCH > STAGE_BYTES) ? BM * C_PITCH : STAGE_BYTES;
 
   __shared__ u32x4 lds_raw[LDS_BYTES / 16];
@@ -697,6 +710,50 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
               dst[e] = zero ? from_f32<TO>(0.f) : from_f32<TO>(to_f32(cv[e]) + to_f32(res[e]));
           }
         }
+      } else if (KB_EPI && p.kb_out != nullptr && vec_ok && n0 >= p.kb_col0 &&
+                 n0 < p.kb_col0 + static_cast<int64_t>(p.kb_heads) * p.kb_hd) {
+        if constexpr (KB_EPI) {
+          // A tile of the K block: the copy also forms each key's |k|^2 per head from the rounded
+          // outputs in the order of the attention's bound pass (an FMA chain over each 16-byte
+          // chunk, then a butterfly over the head's kb_hd / 8 chunks: lanes c ^ off hold chunk
+          // c ^ off of the same row), so the bounds are the same bits as that pass writes. The host
+          // guarantees whole tiles here (M a multiple of 256, kb_seq of 256, kb_col0 of 256).
+          const int lk = p.kb_hd / 8;
+          float kb_m = 0.f;
+          int kb_bad = 0;
+#pragma unroll 4
+          for (int idx = tid; idx < BM * CPR; idx += NT) {
+            const int r = idx / CPR, c = idx % CPR;
+            const int64_t m = m0 + r, n = n0 + static_cast<int64_t>(c) * EPC_OUT;
+            const u32x4 chunk = *reinterpret_cast<const u32x4*>(cl + r * C_PITCH + c * 16);
+            *reinterpret_cast<u32x4*>(static_cast<TO*>(p.C) + m * p.ldc + n) = chunk;
+            const TO* cv = reinterpret_cast<const TO*>(&chunk);
+            float ss = 0.f;
+#pragma unroll
+            for (int e = 0; e < EPC_OUT; ++e) {
+              const float x = to_f32(cv[e]);
+              ss = __builtin_fmaf(x, x, ss);
+            }
+            for (int off = lk / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
+            kb_m = __builtin_elementwise_maximum(kb_m, ss);
+            kb_bad |= p.kb_valid != nullptr && p.kb_valid[m] == 0;
+          }
+          // every chunk column c = tid % CPR is one head's; the two rows of a wave pass meet here
+          __shared__ float kb_red[NT / 64][CPR];
+          kb_m = __builtin_elementwise_maximum(kb_m, __shfl_xor(kb_m, 32));
+          if (lane < CPR) kb_red[wave][lane] = kb_m;
+          const bool bad = __syncthreads_or(kb_bad) != 0;
+          const int heads = BN / p.kb_hd;
+          if (tid < heads) {
+            float v = kb_red[0][tid * lk];
+#pragma unroll
+            for (int w = 1; w < NT / 64; ++w) v = __builtin_elementwise_maximum(v, kb_red[w][tid * lk]);
+            v = __builtin_fabsf(__builtin_sqrtf(v));
+            const int64_t chunks = p.kb_seq / 256, bb = m0 / p.kb_seq, ci = (m0 % p.kb_seq) / 256;
+            const int64_t hh = (n0 - p.kb_col0) / p.kb_hd + tid;
+            p.kb_out[(bb * p.kb_heads + hh) * chunks + ci] = bad ? -v : v;
+          }
+        }
       } else
       for (int idx = tid; idx < BM * CPR; idx += NT) {
         const int r = idx / CPR, c = idx % CPR;
@@ -848,8 +905,14 @@ template <typename T, typename TO, int BM, int BN, int WM, int WN, bool INT8>
 int launch_gemm(const GemmArgs& a, hipStream_t stream) {
   if constexpr (!INT8 && sizeof(T) == 2) {
     // small 16-bit problems: the split-K kernel (see gemm_splitk)
-    if (((a.M + 31) / 32) * ((a.N + 31) / 32) <= 512) return launch_gemm_splitk<T, TO>(a, stream);
+    if (((a.M + 31) / 32) * ((a.N + 31) / 32) <= 512) {
+      if (a.kb_out) return MI355_E_UNSUPPORTED;  // no key-bound epilogue there
+      return launch_gemm_splitk<T, TO>(a, stream);
+    }
   }
+  // the key-bound epilogue: 16-bit outputs of the 256 x 256 tiles
+  if (a.kb_out && (INT8 || sizeof(T) != 2 || sizeof(TO) != 2 || BM != 256 || BN != 256))
+    return MI355_E_UNSUPPORTED;
   const int64_t tiles = ((a.M + BM - 1) / BM) * ((a.N + BN - 1) / BN);
   if (tiles <= 0) return MI355_OK;
   if (tiles > 0x7fffffffLL) return MI355_E_BAD_SIZE;
@@ -878,6 +941,7 @@ int launch_gemm(const GemmArgs& a, hipStream_t stream) {
     constexpr bool LNF_TO = __is_same(T, TO) || __is_same(TO, _Float16);
     const bool lnf = a.ln_stats != nullptr;
     if (persist && (LNF_TO || !lnf)) {
+      if (a.kb_out) return MI355_E_UNSUPPORTED;  // the persistent epilogue has no key bounds
       if constexpr (sizeof(T) == 2) {
         const dim3 pgrid(static_cast<unsigned>(ncu));
         if (lnf) {
@@ -953,7 +1017,8 @@ namespace {
 int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, const void* W, int64_t ldw,
                    const float* bias, const void* R, int64_t ldr, void* C, int64_t ldc, int64_t M,
                    int64_t N, int64_t K, const uint8_t* row_valid, void* stream, int epi = 0,
-                   const float* ln_stats = nullptr, const float* ln_colsum = nullptr) {
+                   const float* ln_stats = nullptr, const float* ln_colsum = nullptr,
+                   const GemmArgs* kb = nullptr) {
   if (M < 0 || N < 0 || K < 0) return MI355_E_BAD_SIZE;
   if (M == 0 || N == 0) return MI355_OK;
   if (!A || !W || !C) return MI355_E_NULL_POINTER;
@@ -985,7 +1050,16 @@ int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, cons
   a.epi = epi;
   a.ln_stats = ln_stats;
   a.ln_colsum = ln_colsum;
+  if (kb) {
+    a.kb_out = kb->kb_out;
+    a.kb_valid = kb->kb_valid;
+    a.kb_col0 = kb->kb_col0;
+    a.kb_seq = kb->kb_seq;
+    a.kb_hd = kb->kb_hd;
+    a.kb_heads = kb->kb_heads;
+  }
   hipStream_t s = static_cast<hipStream_t>(stream);
+  if (a.kb_out && in_dtype == MI355_F32) return MI355_E_UNSUPPORTED;
   switch (in_dtype) {
     case MI355_F16: return launch_by_out<_Float16, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
     case MI355_BF16: return launch_by_out<__bf16, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
@@ -1043,6 +1117,49 @@ extern "C" int mi355_gemm_bias_residual_zero_masked(int in_dtype, int out_dtype,
 }
 
 namespace {
+// Checks of the key-bound arguments (mi355_*_kbound); fills kb's key-bound fields. The epilogue
+// writes whole 256-key chunks with plain stores, so a chunk must be one tile's rows (seq_len a
+// multiple of 256) and a tile's columns whole heads of the K block (k_col0 and n_heads *
+// head_dim multiples of 256); its 16-byte copy path needs 16-byte aligned output rows.
+int kb_args(GemmArgs& kb, int out_dtype, const void* C, int64_t ldc, int64_t M, int64_t N,
+            float* key_bounds, int64_t k_col0, int64_t n_heads, int64_t head_dim, int64_t seq_len,
+            const uint8_t* key_valid) {
+  if (!key_bounds) return MI355_E_NULL_POINTER;
+  if (reinterpret_cast<uintptr_t>(key_bounds) & 3u) return MI355_E_ALIGNMENT;
+  if (n_heads <= 0 || seq_len <= 0 || k_col0 < 0 || n_heads > (1 << 20)) return MI355_E_BAD_SIZE;
+  if (head_dim != 32 && head_dim != 64 && head_dim != 128) return MI355_E_HEAD_DIM;
+  if (k_col0 + n_heads * head_dim > N || M % seq_len != 0) return MI355_E_BAD_SIZE;
+  if (out_dtype != MI355_F16 && out_dtype != MI355_BF16) return MI355_E_UNSUPPORTED;
+  if (seq_len % 256 != 0 || k_col0 % 256 != 0 || (n_heads * head_dim) % 256 != 0)
+    return MI355_E_UNSUPPORTED;
+  if (ldc % 8 != 0 || !aligned16(C)) return MI355_E_UNSUPPORTED;
+  kb.kb_out = key_bounds;
+  kb.kb_valid = key_valid;
+  kb.kb_col0 = k_col0;
+  kb.kb_seq = seq_len;
+  kb.kb_hd = static_cast<int>(head_dim);
+  kb.kb_heads = static_cast<int>(n_heads);
+  return MI355_OK;
+}
+}  // namespace
+
+extern "C" int mi355_gemm_bias_kbound(int in_dtype, int out_dtype, const void* A, int64_t lda,
+                                      const void* W, int64_t ldw, const float* bias, void* C,
+                                      int64_t ldc, int64_t M, int64_t N, int64_t K,
+                                      float* key_bounds, int64_t k_col0, int64_t n_heads,
+                                      int64_t head_dim, int64_t seq_len,
+                                      const uint8_t* key_valid, void* stream) {
+  if (M < 0 || N < 0 || K < 0) return MI355_E_BAD_SIZE;
+  if (M == 0 || N == 0) return MI355_OK;
+  GemmArgs kb{};
+  const int rc = kb_args(kb, out_dtype, C, ldc, M, N, key_bounds, k_col0, n_heads, head_dim,
+                         seq_len, key_valid);
+  if (rc != MI355_OK) return rc;
+  return gemm_bias_impl(in_dtype, out_dtype, A, lda, W, ldw, bias, nullptr, 0, C, ldc, M, N, K,
+                        nullptr, stream, 0, nullptr, nullptr, &kb);
+}
+
+namespace {
 // Checks shared by the LayerNorm-folded entry points; 0 when the arguments are acceptable.
 int ln_gemm_check(int in_dtype, int out_dtype, const void* X, int64_t ldx, const void* W,
                   const float* colsum, float eps, void* C, int64_t M, int64_t N, int64_t K, int epi) {
@@ -1064,12 +1181,14 @@ int ln_gemm_check(int in_dtype, int out_dtype, const void* X, int64_t ldx, const
 
 int ln_gemm_run(int in_dtype, int out_dtype, const void* X, int64_t ldx, const void* W, int64_t ldw,
                 const float* colsum, const float* bias, float eps, float* stats, void* C,
-                int64_t ldc, int64_t M, int64_t N, int64_t K, int epi, void* stream) {
+                int64_t ldc, int64_t M, int64_t N, int64_t K, int epi, void* stream,
+                const GemmArgs* kb = nullptr) {
   hipStream_t s = static_cast<hipStream_t>(stream);
   int rc = mi355_internal_ln_stats(in_dtype, X, ldx, eps, stats, M, K, s);
   if (rc != MI355_OK) return rc;
   return gemm_bias_impl(in_dtype, out_dtype, X, ldx, W, ldw, bias, nullptr, 0, C, ldc, M, N, K,
-                        nullptr, stream, (epi & MI355_EPI_GELU) ? EPI_GELU : 0, stats, colsum);
+                        nullptr, stream, (epi & MI355_EPI_GELU) ? EPI_GELU : 0, stats, colsum,
+                        kb);
 }
 }  // namespace
 
@@ -1084,6 +1203,28 @@ extern "C" int mi355_layernorm_gemm_bias(int in_dtype, int out_dtype, const void
   if (reinterpret_cast<uintptr_t>(stats) & 7u) return MI355_E_ALIGNMENT;
   return ln_gemm_run(in_dtype, out_dtype, X, ldx, W, ldw, colsum, bias, eps, stats, C, ldc, M, N,
                      K, epi, stream);
+}
+
+extern "C" int mi355_layernorm_gemm_bias_kbound(int in_dtype, int out_dtype, const void* X,
+                                                int64_t ldx, const void* W, int64_t ldw,
+                                                const float* colsum, const float* bias, float eps,
+                                                float* stats, void* C, int64_t ldc, int64_t M,
+                                                int64_t N, int64_t K, float* key_bounds,
+                                                int64_t k_col0, int64_t n_heads, int64_t head_dim,
+                                                int64_t seq_len, const uint8_t* key_valid,
+                                                void* stream) {
+  int rc = ln_gemm_check(in_dtype, out_dtype, X, ldx, W, colsum, eps, C, M, N, K, 0);
+  if (rc != MI355_OK || M == 0 || N == 0) return rc;
+  if (!stats) return MI355_E_NULL_POINTER;
+  if (reinterpret_cast<uintptr_t>(stats) & 7u) return MI355_E_ALIGNMENT;
+  GemmArgs kb{};
+  rc = kb_args(kb, out_dtype, C, ldc, M, N, key_bounds, k_col0, n_heads, head_dim, seq_len,
+               key_valid);
+  if (rc != MI355_OK) return rc;
+  // the key-bound epilogue runs on 16-bit operands only: refuse before the statistics pass
+  if (in_dtype == MI355_F32) return MI355_E_UNSUPPORTED;
+  return ln_gemm_run(in_dtype, out_dtype, X, ldx, W, ldw, colsum, bias, eps, stats, C, ldc, M, N,
+                     K, 0, stream, &kb);
 }
 
 // ---- the allocation-free variant: row statistics in a file-scope device array

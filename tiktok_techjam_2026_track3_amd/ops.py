@@ -6,11 +6,51 @@ device. Nothing here synchronises the host, so the calls are hipGraph-capturable
 """
 from __future__ import annotations
 
+from dataclasses import dataclass
 from typing import Optional, Tuple
 
 import torch
 
 from . import _lib
+
+# status of an entry point that cannot run the requested combination (nothing launched)
+_E_UNSUPPORTED = -6
+
+
+@dataclass
+class KeyBoundTarget:
+    """Where a QKV projection writes the attention's key-norm bounds (``mi355_*_kbound``).
+
+    ``workspace`` is the attention workspace (uint8, ``attention_workspace``), whose bound
+    section the projection fills for the K block: output columns ``[k_col0, k_col0 + heads *
+    head_dim)`` of ``seq`` tokens per batch row, with ``key_valid`` ([B, seq] bool, optional)
+    marking chunks that hold an invalid key. ``written`` tells whether the projection wrote
+    them (the fused epilogue has shape requirements; otherwise the attention runs its own pass).
+    """
+    workspace: torch.Tensor
+    k_col0: int
+    heads: int
+    head_dim: int
+    seq: int
+    key_valid: Optional[torch.Tensor] = None
+    written: bool = False
+
+    def _args(self, M: int):
+        if self.workspace.dtype != torch.uint8 or self.workspace.dim() != 1:
+            raise ValueError("the key-bound workspace is a 1-D uint8 tensor")
+        kv = _mask_ptr(self.key_valid, (M // self.seq, self.seq)) if M % self.seq == 0 and \
+            self.key_valid is not None else 0
+        return (self.workspace.data_ptr(), self.k_col0, self.heads, self.head_dim, self.seq, kv)
+
+
+def attention_workspace(B: int, S_q: int, S_k: int, H: int, head_dim: int, dtype: torch.dtype,
+                        device: torch.device) -> torch.Tensor:
+    """A workspace for ``attention(..., workspace=...)`` on ``[B, S, H, head_dim]`` problems of
+    ``dtype``: the key-norm bounds and the redo flags (``mi355_attn_workspace_bytes_forced``);
+    empty when the problem does not run on the matrix-core kernel."""
+    n = _lib.lib().mi355_attn_workspace_bytes_forced(_lib.dtype_code(dtype), B, H, S_q, S_k,
+                                                     head_dim)
+    return torch.empty((max(int(n), 0),), device=device, dtype=torch.uint8)
 
 
 def _stream(t: torch.Tensor) -> int:
@@ -47,7 +87,8 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
            out: Optional[torch.Tensor] = None, row_valid: Optional[torch.Tensor] = None,
            out_dtype: Optional[torch.dtype] = None,
            residual: Optional[torch.Tensor] = None, gelu: bool = False,
-           zero_masked_rows: bool = False) -> torch.Tensor:
+           zero_masked_rows: bool = False,
+           key_bounds: Optional[KeyBoundTarget] = None) -> torch.Tensor:
     """``out[M, N] = x[M, K] @ weight[N, K]^T + bias[N]`` (nn.Linear), fp32 accumulate.
 
     ``x`` may be a row-strided 2-D view (unit column stride); ``weight`` must be contiguous and
@@ -57,7 +98,9 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
     is ``residual + out_dtype(projection)``, masked rows giving ``residual`` -- or zeros with
     ``zero_masked_rows`` (the block's trailing masked_fill). ``gelu`` applies the exact GELU to
     the projection rounded to out_dtype (``F.gelu(nn.Linear(...)(x))``); it excludes
-    ``residual`` and ``row_valid``.
+    ``residual`` and ``row_valid``. With ``key_bounds`` (a QKV projection; no residual, GELU
+    or row mask) the epilogue also writes the attention's key-norm bounds when the shapes allow
+    (``key_bounds.written``).
     """
     _on_gpu(x, weight, bias, out, row_valid, residual)
     if x.dim() != 2 or weight.dim() != 2:
@@ -101,6 +144,18 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: Optional[torch.Tensor] =
             _mask_ptr(row_valid, (M,)), _stream(x))
         _lib.check(fn, st)
         return out
+    if key_bounds is not None:
+        if row_valid is not None:
+            raise ValueError("the key-bound epilogue takes no row mask")
+        _on_gpu(x, key_bounds.workspace, key_bounds.key_valid)
+        st = _lib.lib().mi355_gemm_bias_kbound(
+            _lib.dtype_code(dt), _lib.dtype_code(odt), x.data_ptr(), x.stride(0),
+            weight.data_ptr(), weight.stride(0), bias.data_ptr() if bias is not None else 0,
+            out.data_ptr(), out.stride(0), M, N, K, *key_bounds._args(M), _stream(x))
+        key_bounds.written = st == 0
+        if st != _E_UNSUPPORTED:
+            _lib.check("mi355_gemm_bias_kbound", st)
+            return out
     st = _lib.lib().mi355_gemm_bias(
         _lib.dtype_code(dt), _lib.dtype_code(odt), x.data_ptr(), x.stride(0), weight.data_ptr(),
         weight.stride(0), bias.data_ptr() if bias is not None else 0, out.data_ptr(),
@@ -179,12 +234,13 @@ def layernorm_linear(x: torch.Tensor, weight: torch.Tensor, colsum: torch.Tensor
                      bias: Optional[torch.Tensor], eps: float = 1e-5,
                      out_dtype: Optional[torch.dtype] = None, gelu: bool = False,
                      out: Optional[torch.Tensor] = None,
-                     stats: Optional[torch.Tensor] = None) -> torch.Tensor:
+                     stats: Optional[torch.Tensor] = None,
+                     key_bounds: Optional[KeyBoundTarget] = None) -> torch.Tensor:
     """``nn.Linear(nn.LayerNorm(x))`` (optionally followed by the exact GELU) without writing the
     normalised rows: ``weight``, ``colsum`` and ``bias`` come from ``fold_layernorm``. ``x`` is a
     2-D row-strided tensor (unit column stride); the row statistics go to ``stats`` ([M, 2] fp32
     workspace, allocated when not given). ``out_dtype`` defaults to x's dtype (a bf16 or fp32
-    input may give fp16)."""
+    input may give fp16). ``key_bounds`` as for ``linear`` (not with ``gelu``)."""
     _on_gpu(x, weight, colsum, bias, out, stats)
     if x.dim() != 2 or weight.dim() != 2 or x.stride(1) != 1:
         raise ValueError("layernorm_linear expects a 2-D x with unit column stride and 2-D weight")
@@ -208,6 +264,19 @@ def layernorm_linear(x: torch.Tensor, weight: torch.Tensor, colsum: torch.Tensor
         stats = torch.empty((M, 2), device=x.device, dtype=torch.float32)
     elif stats.shape != (M, 2) or stats.dtype != torch.float32 or not stats.is_contiguous():
         raise ValueError(f"stats must be a contiguous fp32 tensor of shape ({M}, 2)")
+    if key_bounds is not None:
+        if gelu:
+            raise ValueError("the key-bound epilogue takes no GELU")
+        _on_gpu(x, key_bounds.workspace, key_bounds.key_valid)
+        st = _lib.lib().mi355_layernorm_gemm_bias_kbound(
+            _lib.dtype_code(x.dtype), _lib.dtype_code(odt), x.data_ptr(), x.stride(0),
+            weight.data_ptr(), weight.stride(0), colsum.data_ptr(),
+            bias.data_ptr() if bias is not None else 0, float(eps), stats.data_ptr(),
+            out.data_ptr(), out.stride(0), M, N, K, *key_bounds._args(M), _stream(x))
+        key_bounds.written = st == 0
+        if st != _E_UNSUPPORTED:
+            _lib.check("mi355_layernorm_gemm_bias_kbound", st)
+            return out
     st = _lib.lib().mi355_layernorm_gemm_bias(
         _lib.dtype_code(x.dtype), _lib.dtype_code(odt), x.data_ptr(), x.stride(0),
         weight.data_ptr(), weight.stride(0), colsum.data_ptr(),
@@ -220,7 +289,9 @@ def layernorm_linear(x: torch.Tensor, weight: torch.Tensor, colsum: torch.Tensor
 def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[torch.Tensor] = None,
               scale: Optional[float] = None, causal: bool = False,
               key_valid: Optional[torch.Tensor] = None,
-              key_bound: Optional[bool] = None) -> torch.Tensor:
+              key_bound: Optional[bool] = None,
+              workspace: Optional[torch.Tensor] = None, bounds_ready: bool = False,
+              causal_sweep_min_keys: Optional[int] = None) -> torch.Tensor:
     """Streamed softmax attention over ``[B, S, H, head_dim]`` views (unit head_dim stride).
 
     ``out`` defaults to a new contiguous ``[B, S_q, H, head_dim]`` tensor, whose
@@ -232,6 +303,10 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[t
     ranges), True = always (``mi355_attn_workspace_bytes_forced``), False = never. With the
     workspace, a key mask is resolved on the device: work-groups whose keys are all valid run
     the unmasked sweeps, the others a second, key-masked launch; nothing synchronises the host.
+    ``workspace`` (``attention_workspace``) supplies the workspace instead, with
+    ``bounds_ready`` when a QKV projection already wrote the bounds into it
+    (``KeyBoundTarget``) and ``causal_sweep_min_keys`` the key range from which causal query
+    tiles take the sweeps (``mi355_attn_fwd_kb``; default 32768, the library's choice).
     """
     _on_gpu(q, k, v, out, key_valid)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
@@ -257,6 +332,27 @@ def attention(q: torch.Tensor, k: torch.Tensor, v: torch.Tensor, out: Optional[t
         kv_sb = key_valid.stride(0)
     L = _lib
     code = L.dtype_code(dt)
+    if workspace is not None or bounds_ready or causal_sweep_min_keys is not None:
+        if workspace is None:
+            raise ValueError("bounds_ready / causal_sweep_min_keys need a workspace")
+        _on_gpu(q, workspace)
+        if workspace.dtype != torch.uint8 or workspace.dim() != 1:
+            raise ValueError("workspace must be a 1-D uint8 tensor")
+        need = L.lib().mi355_attn_workspace_bytes_forced(code, B, H, Sq, Sk, D)
+        if workspace.numel() < need:
+            raise ValueError(f"workspace holds {workspace.numel()} bytes, {need} needed")
+        gate = 32768 if causal_sweep_min_keys is None else int(causal_sweep_min_keys)
+        st = L.lib().mi355_attn_fwd_kb(
+            code, q.data_ptr(), k.data_ptr(), v.data_ptr(), out.data_ptr(), B, H, Sq, Sk, D,
+            L.i64_array((q.stride(0), q.stride(1), q.stride(2))),
+            L.i64_array((k.stride(0), k.stride(1), k.stride(2))),
+            L.i64_array((v.stride(0), v.stride(1), v.stride(2))),
+            L.i64_array((out.stride(0), out.stride(1), out.stride(2))),
+            float(scale), 1 if causal else 0, kv_ptr, kv_sb,
+            workspace.data_ptr() if need > 0 else 0, workspace.numel() if need > 0 else 0,
+            1 if (bounds_ready and need > 0) else 0, gate, _stream(q))
+        L.check("mi355_attn_fwd_kb", st)
+        return out
     if key_bound is None:
         ws_bytes = L.lib().mi355_attn_workspace_bytes(code, B, H, Sq, Sk, D)
     elif key_bound:
