@@ -1191,13 +1191,9 @@ __global__ __launch_bounds__(256) void attn_key_bound(AttnArgs p, float* __restr
       }
 #pragma unroll
       for (int u = 0; u < UN; ++u) {
-        const typename Mfma<T>::frag f = __builtin_bit_cast(typename Mfma<T>::frag, v[u]);
-        float ss = 0.f;
-#pragma unroll
-        for (int r = 0; r < 8; ++r) {
-          const float x = to_f32(f[r]);
-          ss = __builtin_fmaf(x, x, ss);
-        }
+        // |k|^2: chunk_sq of this lane's chunk, then the butterfly of chunk_tree across the
+        // key's LK lanes (the same bits as the projection epilogue's serial form)
+        float ss = chunk_sq(__builtin_bit_cast(typename Mfma<T>::frag, v[u]));
 #pragma unroll
         for (int off = LK / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
         m = vmax(m, ss);

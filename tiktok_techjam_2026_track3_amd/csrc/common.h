@@ -158,6 +158,41 @@ MI355_DEVINL float pair_sum(float v) {
 
 MI355_DEVINL int elem_size(int dtype) { return dtype == MI355_F32 ? 4 : 2; }
 
+// Key-norm bounds (the attention's bound pass and the QKV projection's epilogue compute them the
+// same way, so both give the same bits): |k|^2 of a key is a sum over its 16-byte chunks of
+// chunk_sq, a chain of packed dot products accumulated in fp32 (v_dot2_f32_f16 / _bf16, in
+// element-pair order), combined by chunk_tree: the pairing of a butterfly over the LK chunks
+// (offsets LK/2 .. 1), which the bound pass runs across lanes with __shfl_xor and the
+// projection epilogue runs within one thread.
+MI355_DEVINL float chunk_sq(f16x8 f) {
+  float acc = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const f16x2 pr = {f[2 * r], f[2 * r + 1]};
+    acc = __builtin_amdgcn_fdot2(pr, pr, acc, false);
+  }
+  return acc;
+}
+MI355_DEVINL float chunk_sq(bf16x8 f) {
+  float acc = 0.f;
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const bf16x2 pr = {f[2 * r], f[2 * r + 1]};
+    acc = __builtin_amdgcn_fdot2_f32_bf16(pr, pr, acc, false);
+  }
+  return acc;
+}
+// s[0] after the butterfly s[i] += s[i ^ off], off = LK/2 .. 1 (the lower index of each pair is
+// kept; the upper one would hold the same value)
+template <int LK>
+MI355_DEVINL float chunk_tree(float (&s)[LK]) {
+#pragma unroll
+  for (int off = LK / 2; off >= 1; off >>= 1)
+#pragma unroll
+    for (int i = 0; i < off; ++i) s[i] = s[i] + s[i + off];
+  return s[0];
+}
+
 // Buffer load straight into LDS (buffer_load_dwordx4 ... lds): 16 bytes per lane from
 // base + soffset + voffset, landing at LDS lds_base + 16 * lane. The resource covers `bytes` bytes
 // from `base` (the range check includes soffset); dwords past it read as 0. The resource is built in these device functions so its type

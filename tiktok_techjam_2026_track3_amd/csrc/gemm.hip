@@ -591,6 +591,15 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
   // 4 consecutive features, as one 16-byte load when the group is inside N and the arrays are
   // 16-byte aligned, and shared by the TM row blocks.
   char* cl = reinterpret_cast<char*>(lds_raw);
+  // a tile of the K block whose key-norm bounds this epilogue writes (see the end); its key-mask
+  // bytes are requested here, long before they are needed
+  bool kb_tile = false;
+  int kb_bad = 0;
+  if constexpr (KB_EPI) {
+    kb_tile = p.kb_out != nullptr && n0 >= p.kb_col0 &&
+              n0 < p.kb_col0 + static_cast<int64_t>(p.kb_heads) * p.kb_hd;
+    if (kb_tile && tid < BM && p.kb_valid != nullptr) kb_bad = p.kb_valid[m0 + tid] == 0;
+  }
   bool in_m_[TM], valid_[TM];
   float sa_m[TM], mean_m[TM], rstd_m[TM];
 #pragma unroll
@@ -710,50 +719,6 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
               dst[e] = zero ? from_f32<TO>(0.f) : from_f32<TO>(to_f32(cv[e]) + to_f32(res[e]));
           }
         }
-      } else if (KB_EPI && p.kb_out != nullptr && vec_ok && n0 >= p.kb_col0 &&
-                 n0 < p.kb_col0 + static_cast<int64_t>(p.kb_heads) * p.kb_hd) {
-        if constexpr (KB_EPI) {
-          // A tile of the K block: the copy also forms each key's |k|^2 per head from the rounded
-          // outputs in the order of the attention's bound pass (an FMA chain over each 16-byte
-          // chunk, then a butterfly over the head's kb_hd / 8 chunks: lanes c ^ off hold chunk
-          // c ^ off of the same row), so the bounds are the same bits as that pass writes. The host
-          // guarantees whole tiles here (M a multiple of 256, kb_seq of 256, kb_col0 of 256).
-          const int lk = p.kb_hd / 8;
-          float kb_m = 0.f;
-          int kb_bad = 0;
-#pragma unroll 4
-          for (int idx = tid; idx < BM * CPR; idx += NT) {
-            const int r = idx / CPR, c = idx % CPR;
-            const int64_t m = m0 + r, n = n0 + static_cast<int64_t>(c) * EPC_OUT;
-            const u32x4 chunk = *reinterpret_cast<const u32x4*>(cl + r * C_PITCH + c * 16);
-            *reinterpret_cast<u32x4*>(static_cast<TO*>(p.C) + m * p.ldc + n) = chunk;
-            const TO* cv = reinterpret_cast<const TO*>(&chunk);
-            float ss = 0.f;
-#pragma unroll
-            for (int e = 0; e < EPC_OUT; ++e) {
-              const float x = to_f32(cv[e]);
-              ss = __builtin_fmaf(x, x, ss);
-            }
-            for (int off = lk / 2; off >= 1; off >>= 1) ss += __shfl_xor(ss, off);
-            kb_m = __builtin_elementwise_maximum(kb_m, ss);
-            kb_bad |= p.kb_valid != nullptr && p.kb_valid[m] == 0;
-          }
-          // every chunk column c = tid % CPR is one head's; the two rows of a wave pass meet here
-          __shared__ float kb_red[NT / 64][CPR];
-          kb_m = __builtin_elementwise_maximum(kb_m, __shfl_xor(kb_m, 32));
-          if (lane < CPR) kb_red[wave][lane] = kb_m;
-          const bool bad = __syncthreads_or(kb_bad) != 0;
-          const int heads = BN / p.kb_hd;
-          if (tid < heads) {
-            float v = kb_red[0][tid * lk];
-#pragma unroll
-            for (int w = 1; w < NT / 64; ++w) v = __builtin_elementwise_maximum(v, kb_red[w][tid * lk]);
-            v = __builtin_fabsf(__builtin_sqrtf(v));
-            const int64_t chunks = p.kb_seq / 256, bb = m0 / p.kb_seq, ci = (m0 % p.kb_seq) / 256;
-            const int64_t hh = (n0 - p.kb_col0) / p.kb_hd + tid;
-            p.kb_out[(bb * p.kb_heads + hh) * chunks + ci] = bad ? -v : v;
-          }
-        }
       } else
       for (int idx = tid; idx < BM * CPR; idx += NT) {
         const int r = idx / CPR, c = idx % CPR;
@@ -778,6 +743,52 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
           const TO* src = reinterpret_cast<const TO*>(&chunk);
           for (int e = 0; e < EPC_OUT && n + e < p.N; ++e)
             dst[e] = res ? from_f32<TO>(to_f32(src[e]) + to_f32(res[e])) : src[e];
+        }
+      }
+    }
+    if constexpr (KB_EPI) {
+      // A tile of the K block (GemmArgs::kb_out): the key-norm bounds of its BN / kb_hd heads
+      // over its 256 rows, from the staged tile (which the copy above only read). Each thread
+      // takes one head and BM / (threads per head) rows; a key's |k|^2 is chunk_sq over its
+      // chunks combined by chunk_tree (the bound pass's bits); then maxima over the rows, the
+      // waves of the head and, for the sign bit, the key mask of the 256 rows (loaded at the
+      // start of the epilogue). The host guarantees whole tiles (M, kb_seq and kb_col0
+      // multiples of 256) and an unmasked projection into 16-byte aligned rows.
+      if (kb_tile) {
+        using frag16 = typename Mfma<TO>::frag;
+        auto bound_rows = [&](auto lk_c) MI355_LAMBDA_INLINE {
+          constexpr int LK = decltype(lk_c)::value;     // 16-byte chunks per head row
+          constexpr int TPH = NT / (BN / (8 * LK));     // threads per head
+          const int hl = tid / TPH, t = tid % TPH;
+          float m = 0.f;
+#pragma unroll
+          for (int r = t; r < BM; r += TPH) {
+            float sq[LK];
+#pragma unroll
+            for (int j = 0; j < LK; ++j)
+              sq[j] = chunk_sq(__builtin_bit_cast(
+                  frag16, *reinterpret_cast<const u32x4*>(cl + r * C_PITCH + (hl * LK + j) * 16)));
+            m = __builtin_elementwise_maximum(m, chunk_tree<LK>(sq));
+          }
+          return m;
+        };
+        const int lk = p.kb_hd / 8;
+        float m = lk == 4 ? bound_rows(std::integral_constant<int, 4>{})
+                : lk == 8 ? bound_rows(std::integral_constant<int, 8>{})
+                          : bound_rows(std::integral_constant<int, 16>{});
+#pragma unroll
+        for (int off = 32; off >= 1; off >>= 1) m = __builtin_elementwise_maximum(m, __shfl_xor(m, off));
+        __shared__ float kb_red[NT / 64];
+        if (lane == 0) kb_red[wave] = m;
+        const bool any_bad = __syncthreads_or(kb_bad) != 0;
+        const int heads = BN / p.kb_hd, wph = (NT / 64) / heads;  // waves per head
+        if (tid < heads) {
+          float v = kb_red[tid * wph];
+          for (int w = 1; w < wph; ++w) v = __builtin_elementwise_maximum(v, kb_red[tid * wph + w]);
+          v = __builtin_fabsf(__builtin_sqrtf(v));
+          const int64_t chunks = p.kb_seq / 256, bb = m0 / p.kb_seq, ci = (m0 % p.kb_seq) / 256;
+          const int64_t hh = (n0 - p.kb_col0) / p.kb_hd + tid;
+          p.kb_out[(bb * p.kb_heads + hh) * chunks + ci] = any_bad ? -v : v;
         }
       }
     }
