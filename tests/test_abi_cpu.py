@@ -255,3 +255,49 @@ def test_noalloc_rejects_rows_beyond_the_array():
     rc = h.mi355_layernorm_gemm_bias_noalloc(1, 1, fake, 64, fake, 64, fake, fake, 1e-5, fake, 32,
                                              (1 << 20) + 1, 32, 64, 0, None)
     assert rc == codes["MI355_E_BAD_SIZE"]
+
+
+def test_key_bound_entry_points_argument_validation():
+    """mi355_gemm_bias_kbound / mi355_layernorm_gemm_bias_kbound refuse, before any launch,
+    what their epilogue cannot serve (MI355_E_UNSUPPORTED: the caller then runs the plain
+    projection and the attention's bound pass) and malformed bound arguments; mi355_attn_fwd_kb
+    needs a workspace for ready bounds and a non-negative causal sweep length."""
+    L = _lib()
+    h = L.lib()
+    codes = _status_codes()
+    fake = 1 << 20
+    F16, BF16, F32 = 1, 2, 0
+    B, S, d, H, hd = 2, 768, 512, 8, 64
+    M, N, K = B * S, 3 * d, d
+
+    def gemm(in_dt=F16, out_dt=F16, kb=fake, col0=d, heads=H, head_dim=hd, seq=S, ldc=N, m=M):
+        return h.mi355_gemm_bias_kbound(in_dt, out_dt, fake, K, fake, K, fake, fake, ldc, m, N, K,
+                                        kb, col0, heads, head_dim, seq, None, None)
+
+    assert gemm(kb=None) == codes["MI355_E_NULL_POINTER"]
+    assert gemm(kb=fake + 2) == codes["MI355_E_ALIGNMENT"]
+    assert gemm(head_dim=80) == codes["MI355_E_HEAD_DIM"]
+    assert gemm(m=M - 256) == codes["MI355_E_BAD_SIZE"]          # rows not whole sequences
+    assert gemm(col0=2 * d + 256) == codes["MI355_E_BAD_SIZE"]   # K block past the columns
+    assert gemm(seq=700, m=2 * 700) == codes["MI355_E_UNSUPPORTED"]   # chunks straddle tiles
+    assert gemm(col0=384, heads=6) == codes["MI355_E_UNSUPPORTED"]    # K block not on a tile
+    assert gemm(out_dt=F32) == codes["MI355_E_UNSUPPORTED"]
+    assert gemm(in_dt=F32) == codes["MI355_E_UNSUPPORTED"]           # fp32 operands
+    assert gemm(ldc=N + 4) == codes["MI355_E_UNSUPPORTED"]           # rows not 16-byte aligned
+    assert gemm(m=256, seq=256) == codes["MI355_E_UNSUPPORTED"]      # split-K sized problem
+    assert h.mi355_layernorm_gemm_bias_kbound(BF16, F16, fake, K, fake, K, fake, fake, 1e-5, fake,
+                                              fake, N, M, N, K, fake, d, H, hd, 700, None,
+                                              None) == codes["MI355_E_BAD_SIZE"]
+    assert h.mi355_layernorm_gemm_bias_kbound(F32, F16, fake, K, fake, K, fake, fake, 1e-5, fake,
+                                              fake, N, M, N, K, fake, d, H, hd, S, None,
+                                              None) == codes["MI355_E_UNSUPPORTED"]
+    st = L.i64_array((3 * d * S, 3 * d, hd))
+    ost = L.i64_array((d * S, d, hd))
+
+    def attn(ws, nbytes, ready, gate):
+        return h.mi355_attn_fwd_kb(F16, fake, fake, fake, fake, B, H, S, S, hd, st, st, st, ost,
+                                   0.125, 1, None, 0, ws, nbytes, ready, gate, None)
+
+    assert attn(None, 0, 1, 2048) == codes["MI355_E_NULL_POINTER"]
+    assert attn(fake, 1 << 16, 0, -1) == codes["MI355_E_BAD_SIZE"]
+    assert attn(fake, 4, 1, 2048) == codes["MI355_E_BAD_SIZE"]       # smaller than the bounds
