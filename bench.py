@@ -68,6 +68,10 @@ def parse_args():
                          "on the kernels: norm1, QKV, attention, out + residual, norm2, ffn_in + "
                          "GELU, ffn_out + residual + row mask; ffn_dim = 4 d_model (16-bit / fp32 "
                          "configurations)")
+    ap.add_argument("--bf16-core", action="store_true",
+                    help="bf16 models (C3) keep q/k/v, the probabilities and the context in bf16 "
+                         "(the bf16 matrix-core attention kernel) instead of fp16 "
+                         "(SelfAttention.bf16_core_dtype)")
     ap.add_argument("--unfolded", action="store_true",
                     help="with --attention-half / --full-block: run the LayerNorms as their own "
                          "row kernels instead of folding them into the QKV / ffn_in projections")
@@ -776,6 +780,8 @@ def main() -> int:
 
     if args.unfolded:
         SelfAttention.fold_norm = False
+    if args.bf16_core:
+        SelfAttention.bf16_core_dtype = torch.bfloat16
 
     if args.official:
         ids = (sorted(W.OFFICIAL_SHAPES) if args.official == "all"
