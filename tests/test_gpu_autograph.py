@@ -47,6 +47,33 @@ def test_forward_replay_equals_eager(gpu, dtype, causal, masked):
     assert all(outs[i].data_ptr() != outs[j].data_ptr() for i in range(4) for j in range(i))
 
 
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal,S", [(False, 512), (True, 2048)])
+@pytest.mark.parametrize("masked", [False, True])
+def test_forward_replay_with_projection_bounds_equals_eager(gpu, dtype, causal, S, masked):
+    """Shapes where the QKV projection writes the attention's key-norm bounds (S and d multiples
+    of 256; causal from SelfAttention.causal_sweep_min_keys keys on): the captured forward (the
+    projection's bound epilogue, the sweep launch and the redo launch, with their workspace
+    allocated inside the capture) gives the eager bits on every replay, with eager work between
+    replays; with a key mask, the work-groups that see its invalid keys go to the key-masked
+    redo launch in both."""
+    mod = _attn(gpu, dtype)
+    x = _x(gpu, dtype, S=S)
+    mask = None
+    if masked:
+        mask = torch.ones(1, S, dtype=torch.bool, device=gpu)
+        mask[0, S - 200] = False
+    with torch.inference_mode():
+        want = mod.run(x, mask, causal)
+        outs = []
+        for _ in range(4):
+            outs.append(mod(x, mask, causal))
+            mod.run(x, mask, not causal)  # eager work between the replays
+    assert _captured(mod) == 1
+    for o in outs:
+        assert torch.equal(o, want)
+
+
 def test_forward_sees_in_place_updates_and_new_tensors(gpu):
     dtype = torch.float16
     mod = _attn(gpu, dtype)
