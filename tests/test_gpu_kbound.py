@@ -198,3 +198,34 @@ def test_block_causal_bounds_policy_prefix_rows(gpu, dtype):
     r = compare_outputs(exact.float().cpu(), full.float().cpu())
     print("  vs exact running max:", r.summary(), flush=True)
     assert r.passed, r.summary()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16])
+@pytest.mark.parametrize("causal", [False, True])
+def test_block_padding_masks_with_projection_bounds(gpu, dtype, causal):
+    """Padded rows (generate_random_case with padding_ratio > 0, torch_transformer_benchmark.py:
+    254-271) at a shape whose QKV projection writes the bounds (B 2, S 2048, d 256, 4 heads):
+    the chunks holding padded keys carry the sign bit, the work-groups that see them run the
+    key-masked redo launch, the others the sweeps; the block passes the reference's predicate
+    against the fp32 oracle and padded rows are zero."""
+    from tiktok_techjam_2026_track3_amd import SelfAttention
+    from tiktok_techjam_2026_track3_amd import workloads as W
+    B, S, d, H = 2, 2048, 256, 4
+    print(f"padding with projection bounds dtype={dtype} causal={causal}", flush=True)
+    w = W.Workload("pad", B, S, d, H, dtype, causal, False, "normal_inv_d")
+    params = W.round_params(W.make_params(w), dtype)
+    x = W.make_input(w, 79)
+    mask = torch.ones(B, S, dtype=torch.bool)
+    mask[0, 1500:] = False   # row 0 padded from key 1500 on; row 1 unpadded
+    x = x.masked_fill(~mask[..., None], 0)
+    mod = SelfAttention(d, H)
+    mod.load_state_dict(params)
+    mod = mod.to(device=gpu, dtype=dtype)
+    mod.auto_graph = False
+    with torch.inference_mode():
+        out = mod(x.to(gpu), mask.to(gpu), causal)
+    ref = OA.self_attention(x.float(), {k: v.float() for k, v in params.items()}, H, mask, causal)
+    r = compare_outputs(ref, out)
+    print("  vs fp32 oracle:", r.summary(), flush=True)
+    assert r.passed, r.summary()
+    assert torch.all(out.cpu()[~mask] == 0)

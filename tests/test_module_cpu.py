@@ -184,3 +184,35 @@ def test_workload_accounting():
     assert torch.equal(x1, x2) and x1.dtype == torch.float32
     # inputs and weights come from different streams
     assert not torch.allclose(x1[0, :256].reshape(-1)[:100], p["q_proj.weight"].reshape(-1)[:100] * 16)
+
+
+def test_autograph_captures_form_no_reference_cycle():
+    """A module's AutoGraph captures reference the module only weakly, so a dropped module frees
+    its captured graphs at once (by reference counting) instead of leaving them to a later
+    garbage collection, which could run while another graph records and would then free a graph
+    in the middle of that capture. Checked on the CPU with a capture record built the way
+    _Capture builds its references (its graph needs a GPU)."""
+    import gc
+    import weakref
+    from tiktok_techjam_2026_track3_amd import graph as G
+    m = SelfAttention(256, 4)
+    m.__dict__["_mi355_pack"] = (torch.zeros(1),)
+    cap = G._Capture.__new__(G._Capture)
+    cap.caches = [(weakref.ref(mm), k, v) for mm, k, v in G._derived_caches(m)]
+    cap.switch_mods = [weakref.ref(x) for x in G._switch_modules(m)]
+    cap.switches = G._switch_values(G._alive(cap.switch_mods))
+    assert cap.switches == G._switch_values(G._switch_modules(m))
+    ag = G.AutoGraph()
+    ag.entries[("signature",)] = {"cap": cap, "calls": 2, "failed": False}
+    m.__dict__["_autograph"] = ag
+    ref = weakref.ref(cap)
+    was_on = gc.isenabled()
+    gc.disable()
+    try:
+        del m, ag, cap
+        assert ref() is None
+    finally:
+        if was_on:
+            gc.enable()
+    # a switch module that no longer exists gives a sentinel no recorded value equals
+    assert G._switch_values([None]) == ((G._GONE,),)

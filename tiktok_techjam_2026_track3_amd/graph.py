@@ -21,6 +21,7 @@ the module had then, and keeps them alive): calling it with other inputs, after 
 """
 from __future__ import annotations
 
+import gc
 import weakref
 from collections import OrderedDict
 from typing import Optional
@@ -34,6 +35,22 @@ def version_of(t: torch.Tensor) -> int:
     in-place updates under torch.inference_mode cannot be seen: caches keyed on them rely on
     load_state_dict / _apply invalidating explicitly)."""
     return -1 if t.is_inference() else t._version
+
+
+def _record(graph: "torch.cuda.CUDAGraph", fn):
+    """``fn()`` recorded into ``graph``; returns its result. No other graph may be destroyed
+    while this one records (freeing a graph and its memory pool are calls a capture forbids):
+    unreachable objects are collected first, and the garbage collector stays off until the
+    capture ends."""
+    gc.collect()
+    gc_was_on = gc.isenabled()
+    gc.disable()
+    try:
+        with torch.cuda.graph(graph):
+            return fn()
+    finally:
+        if gc_was_on:
+            gc.enable()
 
 
 class GraphedForward:
@@ -58,8 +75,7 @@ class GraphedForward:
                     self._run()
             torch.cuda.current_stream().wait_stream(side)
             self.graph = torch.cuda.CUDAGraph()
-            with torch.cuda.graph(self.graph):
-                self.static_out = self._run()
+            self.static_out = _record(self.graph, self._run)
         self._stamp = self._params_stamp()
         # The graph reads the module's derived weight cache (packed / quantised weights) by
         # address. Holding a reference keeps those tensors alive even if the module drops its
@@ -141,9 +157,22 @@ def _switch_modules(module: nn.Module):
 
 
 def _switch_values(mods) -> tuple:
-    """Current values of those attributes (instance or class), in module order."""
-    return tuple((m.eps,) if isinstance(m, nn.LayerNorm)
+    """Current values of those attributes (instance or class), in module order (a module that no
+    longer exists gives a value no recorded one equals)."""
+    return tuple((_GONE,) if m is None else (m.eps,) if isinstance(m, nn.LayerNorm)
                  else tuple(getattr(m, a) for a in type(m).graph_switches) for m in mods)
+
+
+_GONE = object()
+
+
+def _alive(refs) -> list:
+    """The modules behind weak references (None for a module that no longer exists)."""
+    return [r() for r in refs]
+
+
+def _cache_is(m, k: str, v) -> bool:
+    return m is not None and m.__dict__.get(k) is v
 
 
 class _Capture:
@@ -159,17 +188,19 @@ class _Capture:
                 fn(self.static_x, self.static_mask)
         torch.cuda.current_stream().wait_stream(side)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
-            self.static_out = fn(self.static_x, self.static_mask)
+        self.static_out = _record(self.graph, lambda: fn(self.static_x, self.static_mask))
         self.epoch = _REGISTRATION_EPOCH[0]
         self.cls = type(module)
         self.params = list(module.parameters())
         self.tracked = [p for p in self.params if not p.is_inference()]
         self.ptrs = [p.data_ptr() for p in self.params]
         self.vers = [p._version for p in self.tracked]
-        self.caches = _derived_caches(module)   # held: keeps what the graph reads alive
-        self.switch_mods = _switch_modules(module)
-        self.switches = _switch_values(self.switch_mods)
+        # the derived weights are held (the graph reads them); the modules only weakly, so a
+        # module and its captures form no reference cycle and a dropped module's graphs are
+        # freed at once rather than by a later garbage collection
+        self.caches = [(weakref.ref(m), k, v) for m, k, v in _derived_caches(module)]
+        self.switch_mods = [weakref.ref(m) for m in _switch_modules(module)]
+        self.switches = _switch_values(_alive(self.switch_mods))
         self.last = (None, None)                # (weak reference, version) of the inputs copied
 
     def current(self, module: nn.Module) -> bool:
@@ -185,13 +216,13 @@ class _Capture:
             if len(now) != len(self.params) or any(a is not b for a, b in zip(now, self.params)):
                 return False
             mods = _switch_modules(module)
-            if len(mods) != len(self.switch_mods) or any(a is not b for a, b in zip(mods, self.switch_mods)):
+            if len(mods) != len(self.switch_mods) or any(a is not b() for a, b in zip(mods, self.switch_mods)):
                 return False
             self.epoch = _REGISTRATION_EPOCH[0]
         return ([p._version for p in self.tracked] == self.vers
                 and [p.data_ptr() for p in self.params] == self.ptrs
-                and all(m.__dict__.get(k) is v for m, k, v in self.caches)
-                and _switch_values(self.switch_mods) == self.switches)
+                and all(_cache_is(m(), k, v) for m, k, v in self.caches)
+                and _switch_values(_alive(self.switch_mods)) == self.switches)
 
     def replay(self, x: torch.Tensor, mask: Optional[torch.Tensor]) -> torch.Tensor:
         # The copy is skipped when the caller hands back the same tensor objects with unchanged
