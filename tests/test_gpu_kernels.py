@@ -41,7 +41,7 @@ def _report(name, err, bound):
 
 # --------------------------------------------------------------------------------- GEMM
 GEMM_SHAPES = [(1, 64, 64), (128, 768, 256), (300, 200, 136), (513, 130, 1024), (2048, 3072, 1024),
-               (1000, 1536, 512)]
+               (1000, 1536, 512), (4096, 4096, 64), (65536, 128, 128)]
 
 
 @pytest.mark.parametrize("dtype,out_dtype", [(torch.float16, torch.float16),
@@ -55,8 +55,10 @@ GEMM_SHAPES = [(1, 64, 64), (128, 768, 256), (300, 200, 136), (513, 130, 1024), 
 @pytest.mark.parametrize("M,N,K", GEMM_SHAPES)
 def test_linear_error_bound(gpu, dtype, out_dtype, M, N, K):
     """Every operand / output type pair, on shapes that take the split-K kernel (at most 512
-    tiles of 32 x 32: the first four), the 256 x 256 (16-bit) or 128 x 128 / 64 x 64 (fp32)
-    tiled kernel, the LDS-DMA loader (K a multiple of the K step) and the register-staged one."""
+    tiles of 32 x 32: the first four), the tiled kernel at each of its 16-bit tile sizes
+    (128 x 128 for 2048 x 3072 and for 65536 x 128, 64 x 64 for 1000 x 1536, 256 x 256 for
+    4096 x 4096 x 64) and at the fp32 ones (128 x 128 / 64 x 64), the LDS-DMA loader (K a multiple
+    of the K step) and the register-staged one."""
     ops = _ops()
     a = _rand((M, K), dtype, 1)
     w = _rand((N, K), dtype, 2, scale=K ** -0.5)

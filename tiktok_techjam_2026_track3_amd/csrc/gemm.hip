@@ -798,6 +798,15 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
 #ifndef MI355_GEMM_DIRECT
 #define MI355_GEMM_DIRECT 1
 #endif
+#ifndef MI355_GEMM_NARROW
+#define MI355_GEMM_NARROW 1
+#endif
+#ifndef MI355_GEMM_FILL
+#define MI355_GEMM_FILL 256
+#endif
+#ifndef MI355_GEMM_FILL64
+#define MI355_GEMM_FILL64 128
+#endif
 
 // Small problems (at most 512 tiles of 32 x 32 outputs: the fp32 configuration's projections
 // are 128 x 768 x 256 and 128 x 256 x 256; the official shapes' small batches), fp32 or 16-bit:
@@ -1071,9 +1080,30 @@ int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, cons
   }
   hipStream_t s = static_cast<hipStream_t>(stream);
   if (a.kb_out && in_dtype == MI355_F32) return MI355_E_UNSUPPORTED;
+  // 16-bit tile: 256 x 256 on 8 waves, or 128 x 128 / 64 x 64 on 4 waves (two or more
+  // work-groups per CU) where 256 x 256 tiles would leave CUs idle (fewer tiles than CUs:
+  // MI355_GEMM_FILL) or compute half padding (at most 128 output features, the official shapes'
+  // d_model 128, short of the persistent regime's tile counts, where 256 x 256 stays faster);
+  // 64 x 64 where even 128 x 128 tiles would not give half the CUs one (MI355_GEMM_FILL64).
+  // Measured against 256 x 256 (one process, one box): 65536 x 128 x 128 44 -> 20 us,
+  // 8192 x 128 x 128 38 -> 11 us (64 x 64), 8192 x 384 x 128 19 -> 15 us, 8192 x 1024 x 1024
+  // 39 -> 31 us; 1280000 x 128 x 128 (persistent) 194 us against 224 us at 128 x 128.
+  int tile = 256;
+  if (MI355_GEMM_NARROW && !a.kb_out) {
+    const int64_t t256 = ((M + 255) / 256) * ((N + 255) / 256);
+    const int64_t t128 = ((M + 127) / 128) * ((N + 127) / 128);
+    if (t256 < MI355_GEMM_FILL || (N <= 128 && t256 < 4 * MI355_GEMM_FILL)) tile = 128;
+    if (tile == 128 && t128 < MI355_GEMM_FILL64) tile = 64;
+  }
   switch (in_dtype) {
-    case MI355_F16: return launch_by_out<_Float16, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
-    case MI355_BF16: return launch_by_out<__bf16, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
+    case MI355_F16:
+      if (tile == 64) return launch_by_out<_Float16, 64, 64, 2, 2, false>(a, s);
+      if (tile == 128) return launch_by_out<_Float16, 128, 128, 2, 2, false>(a, s);
+      return launch_by_out<_Float16, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
+    case MI355_BF16:
+      if (tile == 64) return launch_by_out<__bf16, 64, 64, 2, 2, false>(a, s);
+      if (tile == 128) return launch_by_out<__bf16, 128, 128, 2, 2, false>(a, s);
+      return launch_by_out<__bf16, MI355_GEMM_BM, MI355_GEMM_BN, MI355_GEMM_WM, MI355_GEMM_WN, false>(a, s);
     default: {
       // small problems (the fp32 configuration's projections are 128 x 768 and 128 x 256):
       // 32 x 32 tiles with K split over 8 waves; mid-size ones 64 x 64 tiles
