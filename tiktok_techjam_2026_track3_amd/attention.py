@@ -89,11 +89,13 @@ class SelfAttention(nn.Module):
     # runs fp32 models on fp16 tiles (Project/submission/dispatcher_region.py:1017-1091);
     # torch.float32 keeps fp32 operands (the LayerNorms then folded into the projections)
     fp32_operand_dtype = torch.float16
-    # ... from this many input elements on: below it the fp32 path (LayerNorm folded into
-    # 128 x 128-tile fp32 projections) is faster than a LayerNorm launch and 256 x 256-tile fp16
-    # projections that leave most CUs idle (official shapes 1, 5, 9, 10: 8192 x 128 tokens x
-    # features, 0.49-0.55 ms against 0.63-0.66 ms per forward)
-    fp16_operand_min_elems = 1 << 23
+    # ... from this many input elements on (0: always). The fp16 projections take tiles sized to
+    # the problem (128 x 128 / 64 x 64 on small ones), so they beat the fp32 path (LayerNorm
+    # folded into 128 x 128-tile fp32 projections) at every size measured: official shapes 1, 5,
+    # 9, 10 (8192-16384 tokens of 128 features) 0.34-0.41 -> 0.21-0.30 ms per forward, shapes
+    # 2-4 and 12 8-12% faster. (With 256 x 256 fp16 tiles only, the fp32 path had been faster
+    # below 2^23 elements.)
+    fp16_operand_min_elems = 0
 
     def operand_dtype(self, dtype: torch.dtype, numel: int = 1 << 62) -> torch.dtype:
         """Operand dtype of the block's projections (forward_residual, the FFN half) for model
