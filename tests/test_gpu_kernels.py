@@ -280,9 +280,12 @@ def test_attention_other_head_dims_masked_packed(gpu, dtype, hd, causal):
 # --------------------------------------------------------------------------------- int8
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("mode", [0, 1])
-def test_quant_rows_bit_exact(gpu, dtype, mode):
+@pytest.mark.parametrize("K", [512, 4096, 4000, 16384])
+def test_quant_rows_bit_exact(gpu, dtype, mode, K):
+    """Row lengths that keep the row in registers (64 * 2^i 16-byte chunks up to 16 per lane:
+    512 and 4096, and 16384 for fp32) and that take the two-pass kernel (4000; 16384 16-bit)."""
     ops = _ops()
-    x = _rand((300, 4096), dtype, 41, scale=0.7)
+    x = _rand((300, K), dtype, 41, scale=0.7)
     x[3] = 0                                   # zero row exercises the clamp
     x[4, :16] = torch.tensor([2.5, -2.5, 0.5, 1.5] * 4, dtype=dtype)
     q, s = ops.quant_rows_i8(x.to(gpu), mode=mode)
