@@ -807,6 +807,11 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
 #ifndef MI355_GEMM_FILL64
 #define MI355_GEMM_FILL64 128
 #endif
+// fp32 operands: 64 x 64 tiles below this many 128 x 128 tiles (one per CU: official shape 11,
+// whose fp32 projections are 8192 x 384 / 128 x 128, 0.45 -> 0.33 ms per forward against 64)
+#ifndef MI355_GEMM_F32_FILL
+#define MI355_GEMM_F32_FILL 256
+#endif
 
 // Small problems (at most 512 tiles of 32 x 32 outputs: the fp32 configuration's projections
 // are 128 x 768 x 256 and 128 x 256 x 256; the official shapes' small batches), fp32 or 16-bit:
@@ -1111,11 +1116,11 @@ int gemm_bias_impl(int in_dtype, int out_dtype, const void* A, int64_t lda, cons
       const int64_t tiles128 = ((a.M + 127) / 128) * ((a.N + 127) / 128);
       if (out_dtype == MI355_F16) {
         if (tiles32 <= 512) return launch_gemm_splitk<float, _Float16>(a, s);
-        if (tiles128 < 64) return launch_gemm<float, _Float16, 64, 64, 2, 2, false>(a, s);
+        if (tiles128 < MI355_GEMM_F32_FILL) return launch_gemm<float, _Float16, 64, 64, 2, 2, false>(a, s);
         return launch_gemm<float, _Float16, 128, 128, 2, 2, false>(a, s);
       }
       if (tiles32 <= 512) return launch_gemm_splitk<float, float>(a, s);
-      if (tiles128 < 64) return launch_gemm<float, float, 64, 64, 2, 2, false>(a, s);
+      if (tiles128 < MI355_GEMM_F32_FILL) return launch_gemm<float, float, 64, 64, 2, 2, false>(a, s);
       return launch_gemm<float, float, 128, 128, 2, 2, false>(a, s);
     }
   }
