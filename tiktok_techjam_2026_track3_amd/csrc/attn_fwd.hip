@@ -188,6 +188,15 @@ MI355_DEVINL int swz(int r) {
 #ifndef MI355_ATTN_MFPIPE
 #define MI355_ATTN_MFPIPE 1
 #endif
+// Issue priority by progress (1) in the pipelined branch-free sweep: a wave runs the first half of
+// its stages at priority 1 and the rest at 0. Two work-groups share a CU (one wave of each per
+// SIMD), and at equal priority the SIMD issues from the older wave, so of two work-groups that
+// start together one finished far earlier (C2: ~50 against ~70 us) and the launch ended with CUs
+// running one wave per SIMD; with the priority falling at half way, the work-group that is behind
+// issues first for a while (C2 +3%, C5 +0.6%, outputs unchanged).
+#ifndef MI355_ATTN_PROGPRIO
+#define MI355_ATTN_PROGPRIO 1
+#endif
 // output rows staged through LDS and stored as 16-byte chunks (1) or stored as 8-byte runs (0)
 #ifndef MI355_ATTN_OSTAGE
 #define MI355_ATTN_OSTAGE 1
@@ -1037,6 +1046,14 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
           };
           if (st + U - 1 < n_main) {
             score_u(sA, 0, 0, 0);
+            if constexpr (MI355_ATTN_PROGPRIO && !PRIO) {
+              // two copies of the loop, so that no branch sits between trips (a branch there, or
+              // more copies, made the instances spill): the first half of the stages at
+              // priority 1, the rest at 0
+              __builtin_amdgcn_s_setprio(1);
+              for (; st + 2 * U - 1 < n_main && 2 * st < n_st; st += U) trip(st, std::true_type{});
+              __builtin_amdgcn_s_setprio(0);
+            }
             for (; st + 2 * U - 1 < n_main; st += U) trip(st, std::true_type{});
             trip(st, std::false_type{});
             st += U;
