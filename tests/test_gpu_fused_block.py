@@ -52,8 +52,9 @@ def _ulp(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
 
 # ------------------------------------------------------------------------------- LayerNorm
 # row lengths up to each dtype's one-wave limit (8192 16-bit or 4096 fp32 elements)
+# (K = 32 .. 256: rows of 8 / 16 / 32 vectors share a wave, 8 / 4 / 2 rows per wave)
 LN_CASES = [(dt, K) for dt in (torch.float16, torch.bfloat16, torch.float32)
-            for K in (64, 256, 1000, 2048, 4096, 8192) if not (dt == torch.float32 and K > 4096)]
+            for K in (32, 64, 128, 256, 1000, 2048, 4096, 8192) if not (dt == torch.float32 and K > 4096)]
 
 
 @pytest.mark.parametrize("dtype,K", LN_CASES)

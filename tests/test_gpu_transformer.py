@@ -105,7 +105,8 @@ def test_residual_zero_masked_bit_exact(gpu, dtype, M, N, K):
 
 
 @pytest.mark.parametrize("dtype,K", [(torch.float16, 1024), (torch.bfloat16, 2048),
-                                     (torch.float32, 256), (torch.float16, 4096)])
+                                     (torch.float32, 256), (torch.float16, 4096),
+                                     (torch.float32, 128), (torch.float16, 64), (torch.float32, 32)])
 def test_layer_norm_masked_rows(gpu, dtype, K):
     from tiktok_techjam_2026_track3_amd import ops
     g = torch.Generator().manual_seed(K)

@@ -1,21 +1,26 @@
 // Row LayerNorm (nn.LayerNorm over the last dimension) for gfx950:
 //   y = (x - mean) * rstd * gamma + beta,  rstd = 1 / sqrt(var + eps),  var biased (divide by K)
-// Statistics and the affine map are fp32; y is rounded once to the input dtype. One wave per row,
-// the row held in registers as 16-byte vectors (up to 64 * NV vectors), two-pass mean / variance.
-// HBM-bound: reads the row once and writes it once.
+// Statistics and the affine map are fp32; y is rounded once to the input dtype. G lanes per row
+// (G = 64: one wave per row; rows of at most 32 16-byte vectors share a wave, 64 / G rows per
+// wave, so that short rows keep every lane busy), the row held in registers as 16-byte vectors
+// (up to G * NV vectors), two-pass mean / variance. HBM-bound: reads the row once and writes it
+// once.
 #include "common.h"
 
 namespace {
 
-MI355_DEVINL float wave_sum(float v) {
+// sum over the G lanes of a row group (lanes g*G .. g*G + G - 1): butterfly over offsets < G.
+// A row of n < G vectors leaves lanes n.. at 0, so the sum has the bits of the 64-lane tree.
+template <int G>
+MI355_DEVINL float group_sum(float v) {
 #pragma unroll
-  for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+  for (int off = G / 2; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
   return v;
 }
 
 // TO: output type (the input type, or fp16 for an fp32 input: the fp16 operands of an fp32
 // model's projections)
-template <typename T, int NV, typename TO = T>
+template <typename T, int NV, int G, typename TO = T>
 __global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, int64_t ldx,
                                                       const T* __restrict__ gamma,
                                                       const T* __restrict__ beta, float eps,
@@ -24,14 +29,14 @@ __global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, i
   constexpr int EPV = 16 / static_cast<int>(sizeof(T));  // elements per 16-byte vector
   typedef T tv __attribute__((ext_vector_type(EPV)));
   typedef TO tov __attribute__((ext_vector_type(EPV)));
-  const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
-  if (row >= M) return;  // whole wave leaves together
+  const int lane = threadIdx.x % G;  // lane within the row group
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / G) + threadIdx.x / G;
+  if (row >= M) return;  // the row group leaves together (its shuffles stay inside it)
   const int nvec = K / EPV;
   if (row_valid != nullptr && row_valid[row] == 0) {
     // masked row: zeros (the masked_fill that follows the final norm)
     TO* yr = Y + row * ldy;
-    for (int vi = lane; vi < nvec; vi += 64) *reinterpret_cast<tov*>(yr + static_cast<int64_t>(vi) * EPV) = tov{};
+    for (int vi = lane; vi < nvec; vi += G) *reinterpret_cast<tov*>(yr + static_cast<int64_t>(vi) * EPV) = tov{};
     return;
   }
   const T* xr = X + row * ldx;
@@ -40,7 +45,7 @@ __global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, i
   float sum = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int vi = lane + 64 * j;
+    const int vi = lane + G * j;
     tv v = {};
     if (vi < nvec) v = *reinterpret_cast<const tv*>(xr + static_cast<int64_t>(vi) * EPV);
 #pragma unroll
@@ -49,11 +54,11 @@ __global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, i
       sum += xs[j][e];
     }
   }
-  const float mean = wave_sum(sum) / static_cast<float>(K);
+  const float mean = group_sum<G>(sum) / static_cast<float>(K);
   float sq = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    if (lane + 64 * j < nvec) {
+    if (lane + G * j < nvec) {
 #pragma unroll
       for (int e = 0; e < EPV; ++e) {
         const float d = xs[j][e] - mean;
@@ -61,13 +66,13 @@ __global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, i
       }
     }
   }
-  const float var = wave_sum(sq) / static_cast<float>(K);
+  const float var = group_sum<G>(sq) / static_cast<float>(K);
   const float rstd = 1.0f / sqrtf(var + eps);
 
   TO* yr = Y + row * ldy;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int vi = lane + 64 * j;
+    const int vi = lane + G * j;
     if (vi >= nvec) continue;
     tv gv, bv;
     if (gamma) gv = *reinterpret_cast<const tv*>(gamma + static_cast<int64_t>(vi) * EPV);
@@ -90,13 +95,13 @@ __global__ __launch_bounds__(256) void layernorm_rows(const T* __restrict__ X, i
 // variance is exactly 0 (every element equals the mean, so its normalised values are exactly
 // beta) gets rstd 0: the folded epilogue then yields the bias term alone instead of
 // 1/sqrt(eps) times the fp32 rounding residue of x W'^T - mean colsum.
-template <typename T, int NV>
+template <typename T, int NV, int G>
 __global__ __launch_bounds__(256) void layernorm_stats(const T* __restrict__ X, int64_t ldx, float eps,
                                                        float* __restrict__ stats, int64_t M, int K) {
   constexpr int EPV = 16 / static_cast<int>(sizeof(T));
   typedef T tv __attribute__((ext_vector_type(EPV)));
-  const int lane = threadIdx.x & 63;
-  const int64_t row = static_cast<int64_t>(blockIdx.x) * 4 + (threadIdx.x >> 6);
+  const int lane = threadIdx.x % G;
+  const int64_t row = static_cast<int64_t>(blockIdx.x) * (256 / G) + threadIdx.x / G;
   if (row >= M) return;
   const int nvec = K / EPV;
   const T* xr = X + row * ldx;
@@ -104,7 +109,7 @@ __global__ __launch_bounds__(256) void layernorm_stats(const T* __restrict__ X, 
   float sum = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    const int vi = lane + 64 * j;
+    const int vi = lane + G * j;
     tv v = {};
     if (vi < nvec) v = *reinterpret_cast<const tv*>(xr + static_cast<int64_t>(vi) * EPV);
 #pragma unroll
@@ -113,11 +118,11 @@ __global__ __launch_bounds__(256) void layernorm_stats(const T* __restrict__ X, 
       sum += xs[j][e];
     }
   }
-  const float mean = wave_sum(sum) / static_cast<float>(K);
+  const float mean = group_sum<G>(sum) / static_cast<float>(K);
   float sq = 0.f;
 #pragma unroll
   for (int j = 0; j < NV; ++j) {
-    if (lane + 64 * j < nvec) {
+    if (lane + G * j < nvec) {
 #pragma unroll
       for (int e = 0; e < EPV; ++e) {
         const float d = xs[j][e] - mean;
@@ -125,33 +130,44 @@ __global__ __launch_bounds__(256) void layernorm_stats(const T* __restrict__ X, 
       }
     }
   }
-  const float var = wave_sum(sq) / static_cast<float>(K);
+  const float var = group_sum<G>(sq) / static_cast<float>(K);
   if (lane == 0) {
     typedef float f32x2 __attribute__((ext_vector_type(2)));
     *reinterpret_cast<f32x2*>(stats + 2 * row) = f32x2{mean, var > 0.f ? 1.0f / sqrtf(var + eps) : 0.f};
   }
 }
 
+// lanes per row: rows of at most 8 / 16 / 32 vectors take that many lanes (8 / 4 / 2 rows per
+// wave), longer rows a whole wave
+inline int lanes_per_row(int64_t nvec) { return nvec <= 8 ? 8 : nvec <= 16 ? 16 : nvec <= 32 ? 32 : 64; }
+
 template <typename T>
 int launch_stats(const void* X, int64_t ldx, float eps, float* stats, int64_t M, int64_t K,
                  hipStream_t s) {
   constexpr int EPV = 16 / static_cast<int>(sizeof(T));
   const int64_t nvec = K / EPV;
-  const int64_t blocks = (M + 3) / 4;
+  const int g = lanes_per_row(nvec);
+  const int64_t blocks = (M + 256 / g - 1) / (256 / g);
   if (blocks > 0x7fffffffLL) return MI355_E_BAD_SIZE;
   const dim3 grid(static_cast<unsigned>(blocks)), block(256);
   const T* x = static_cast<const T*>(X);
   const int k = static_cast<int>(K);
-  if (nvec <= 64)
-    hipLaunchKernelGGL((layernorm_stats<T, 1>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+  if (g == 8)
+    hipLaunchKernelGGL((layernorm_stats<T, 1, 8>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+  else if (g == 16)
+    hipLaunchKernelGGL((layernorm_stats<T, 1, 16>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+  else if (g == 32)
+    hipLaunchKernelGGL((layernorm_stats<T, 1, 32>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+  else if (nvec <= 64)
+    hipLaunchKernelGGL((layernorm_stats<T, 1, 64>), grid, block, 0, s, x, ldx, eps, stats, M, k);
   else if (nvec <= 128)
-    hipLaunchKernelGGL((layernorm_stats<T, 2>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+    hipLaunchKernelGGL((layernorm_stats<T, 2, 64>), grid, block, 0, s, x, ldx, eps, stats, M, k);
   else if (nvec <= 256)
-    hipLaunchKernelGGL((layernorm_stats<T, 4>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+    hipLaunchKernelGGL((layernorm_stats<T, 4, 64>), grid, block, 0, s, x, ldx, eps, stats, M, k);
   else if (nvec <= 512)
-    hipLaunchKernelGGL((layernorm_stats<T, 8>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+    hipLaunchKernelGGL((layernorm_stats<T, 8, 64>), grid, block, 0, s, x, ldx, eps, stats, M, k);
   else
-    hipLaunchKernelGGL((layernorm_stats<T, 16>), grid, block, 0, s, x, ldx, eps, stats, M, k);
+    hipLaunchKernelGGL((layernorm_stats<T, 16, 64>), grid, block, 0, s, x, ldx, eps, stats, M, k);
   return static_cast<int>(hipGetLastError());
 }
 
@@ -160,7 +176,8 @@ int launch_ln(const void* X, int64_t ldx, const void* gamma, const void* beta, f
               int64_t ldy, int64_t M, int64_t K, const uint8_t* rv, hipStream_t s) {
   constexpr int EPV = 16 / static_cast<int>(sizeof(T));
   const int64_t nvec = K / EPV;
-  const int64_t blocks = (M + 3) / 4;
+  const int gl = lanes_per_row(nvec);
+  const int64_t blocks = (M + 256 / gl - 1) / (256 / gl);
   if (blocks > 0x7fffffffLL) return MI355_E_BAD_SIZE;
   const dim3 grid(static_cast<unsigned>(blocks)), block(256);
   const T* x = static_cast<const T*>(X);
@@ -168,16 +185,22 @@ int launch_ln(const void* X, int64_t ldx, const void* gamma, const void* beta, f
   const T* b = static_cast<const T*>(beta);
   TO* y = static_cast<TO*>(Y);
   const int k = static_cast<int>(K);
-  if (nvec <= 64)
-    hipLaunchKernelGGL((layernorm_rows<T, 1, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+  if (gl == 8)
+    hipLaunchKernelGGL((layernorm_rows<T, 1, 8, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+  else if (gl == 16)
+    hipLaunchKernelGGL((layernorm_rows<T, 1, 16, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+  else if (gl == 32)
+    hipLaunchKernelGGL((layernorm_rows<T, 1, 32, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+  else if (nvec <= 64)
+    hipLaunchKernelGGL((layernorm_rows<T, 1, 64, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   else if (nvec <= 128)
-    hipLaunchKernelGGL((layernorm_rows<T, 2, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+    hipLaunchKernelGGL((layernorm_rows<T, 2, 64, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   else if (nvec <= 256)
-    hipLaunchKernelGGL((layernorm_rows<T, 4, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+    hipLaunchKernelGGL((layernorm_rows<T, 4, 64, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   else if (nvec <= 512)
-    hipLaunchKernelGGL((layernorm_rows<T, 8, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+    hipLaunchKernelGGL((layernorm_rows<T, 8, 64, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   else
-    hipLaunchKernelGGL((layernorm_rows<T, 16, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
+    hipLaunchKernelGGL((layernorm_rows<T, 16, 64, TO>), grid, block, 0, s, x, ldx, g, b, eps, y, ldy, M, k, rv);
   return static_cast<int>(hipGetLastError());
 }
 
