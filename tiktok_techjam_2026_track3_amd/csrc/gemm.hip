@@ -136,6 +136,12 @@ MI355_DEVINL int swzc(int r) {
 #ifndef MI355_GEMM_NST
 #define MI355_GEMM_NST 2
 #endif
+// persistent tiles of one tile column whose K is one ring turn (N <= 256, K = 128 for 16-bit
+// operands: the d_model-128 projections of the official shapes) keep W's stages in the ring
+// and load only A after the first tile (1), or reload W with every tile (0)
+#ifndef MI355_GEMM_WKEEP
+#define MI355_GEMM_WKEEP 1
+#endif
 
 // XCD-aware work-group order: the dispatcher deals work-groups round-robin to the 8 XCDs, so
 // hand each XCD a contiguous range of logical tiles (shared A rows / W columns stay in its L2),
@@ -290,12 +296,16 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
   // this tile's resources and (PERSIST) the next tile's, whose first stage the last K step loads
   u32x4 a_rsrc, w_rsrc, na_rsrc, nw_rsrc;
   tile_rsrc(m0, n0, a_rsrc, w_rsrc);
+  // PERSIST with one column of tiles and K of exactly one ring turn (N <= BN, nk == NST): every
+  // tile's W stages are the same bytes in the same slots (nothing else writes the ring), so after
+  // the first tile only A is loaded (w_held; MI355_GEMM_WKEEP)
+  bool w_held = false;
   auto load_one = [&](int s, int64_t k0, int i, bool nxt) {
     const uint32_t so = static_cast<uint32_t>(k0) * ES;
     const int blk = wv + i * NWAVE;
     if (i < (BM / RBK) / NWAVE)
       buffer_dma_lds16(nxt ? na_rsrc : a_rsrc, doff[i], so, lds_addr_of(&lds[s][blk * 64]));
-    else
+    else if (!(PERSIST && MI355_GEMM_WKEEP && w_held))
       buffer_dma_lds16(nxt ? nw_rsrc : w_rsrc, doff[i], so, lds_addr_of(&lds[s][blk * 64]));
   };
   auto load_direct = [&](int s, int64_t k0, bool nxt = false) {
@@ -437,10 +447,10 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
       if (!valid[a]) v = 0.f;
       return from_f32<TO>(v);
     };
-    // residual add on the rounded projection (read before the write: R may be C), zeroed rows
-    auto finish = [&](u32x4 chunk, int64_t m, int64_t n, bool ok) MI355_LAMBDA_INLINE {
+    // residual add on the rounded projection (rc: the residual chunk, read before any write of
+    // the block: R may be C), zeroed rows
+    auto finish = [&](u32x4 chunk, int64_t m, int64_t n, bool ok, const u32x4& rc) MI355_LAMBDA_INLINE {
       if (p.R) {
-        const u32x4 rc = *reinterpret_cast<const u32x4*>(static_cast<const TO*>(p.R) + m * p.ldr + n);
         TO* cv = reinterpret_cast<TO*>(&chunk);
         const TO* rv = reinterpret_cast<const TO*>(&rc);
 #pragma unroll
@@ -449,10 +459,27 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
       if (!ok && (p.epi & EPI_ZERO_MASKED)) chunk = u32x4{0u, 0u, 0u, 0u};
       *reinterpret_cast<u32x4*>(static_cast<TO*>(p.C) + m * p.ldc + n) = chunk;
     };
+    // Residual chunks are requested two at a time before the stores that use them (16-bit
+    // outputs: the TM (<= 2) row blocks of a (b, j); fp32 outputs: the two halves h of an
+    // (a, b, j)).
+    // One at a time, each load waited for behind the previous store, the residual had doubled the
+    // epilogue's time (official shape 6's fp32 out projection 0.31 -> 0.59 ms).
+    static_assert(TM <= 2, "at most two residual chunks per batch");
+    auto res_load = [&](u32x4& r, int64_t m, int64_t n, bool in) MI355_LAMBDA_INLINE {
+      r = u32x4{0u, 0u, 0u, 0u};
+      if (p.R && in) r = *reinterpret_cast<const u32x4*>(static_cast<const TO*>(p.R) + m * p.ldr + n);
+    };
 #pragma unroll
     for (int b = 0; b < TN; ++b) {
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
+        u32x4 rres[2];
+        if constexpr (sizeof(TO) == 2) {
+          const int64_t n = n0 + wn * WTN + b * 32 + 16 * j + 8 * g;
+#pragma unroll
+          for (int a = 0; a < TM; ++a)
+            res_load(rres[a], m0 + wm * WTM + a * 32 + l32, n, in_m[a] && n < p.N);
+        }
         const int64_t nb = n0 + wn * WTN + b * 32 + 16 * j + 4 * g;  // group i4 = 2j; 2j + 1 at +8
         const f32x4 bias0 = col4(p.bias, nb), bias1 = col4(p.bias, nb + 8);
         const f32x4 cs0 = LNF ? col4(p.ln_colsum, nb) : f32x4{0.f, 0.f, 0.f, 0.f};
@@ -462,12 +489,15 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
           const int64_t m = m0 + wm * WTM + a * 32 + l32;
           if constexpr (sizeof(TO) == 4) {
 #pragma unroll
+            for (int h = 0; h < 2; ++h) res_load(rres[h], m, nb + 8 * h, in_m[a] && nb + 8 * h < p.N);
+#pragma unroll
             for (int h = 0; h < 2; ++h) {
               f32x4 w;
 #pragma unroll
               for (int e = 0; e < 4; ++e)
                 w[e] = value(a, b, 2 * j + h, e, h ? bias1 : bias0, h ? cs1 : cs0);
-              if (in_m[a] && nb + 8 * h < p.N) finish(__builtin_bit_cast(u32x4, w), m, nb + 8 * h, valid[a]);
+              if (in_m[a] && nb + 8 * h < p.N)
+                finish(__builtin_bit_cast(u32x4, w), m, nb + 8 * h, valid[a], rres[h]);
             }
           } else {
             typedef TO to2 __attribute__((ext_vector_type(2)));
@@ -484,7 +514,7 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
             const auto rh = __builtin_amdgcn_permlane32_swap(hi[0], hi[1], false, false);
             const u32x4 chunk = {rl[0], rh[0], rl[1], rh[1]};
             const int64_t n = n0 + wn * WTN + b * 32 + 16 * j + 8 * g;
-            if (in_m[a] && n < p.N) finish(chunk, m, n, valid[a]);
+            if (in_m[a] && n < p.N) finish(chunk, m, n, valid[a], rres[a]);
           }
         }
       }
@@ -546,6 +576,7 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
         if (kt + u < nk) step(kt + u, u);
     };
     if constexpr (PERSIST) {
+      const bool w_keep = MI355_GEMM_WKEEP && ntn == 1 && nk == NST;
       for (;;) {
         const int64_t npid = pid + gridDim.x;
         has_next = npid < ntm * ntn;
@@ -555,6 +586,8 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
           tile_rsrc(nm0, nn0, na_rsrc, nw_rsrc);
         }
         k_loop();
+        // from here on every W load would rewrite the bytes the slots hold (see w_held)
+        w_held = w_keep;
         epilogue_direct();
         if (!has_next) return;
         pid = npid;
