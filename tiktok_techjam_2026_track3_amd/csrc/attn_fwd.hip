@@ -188,6 +188,10 @@ MI355_DEVINL int swz(int r) {
 #ifndef MI355_ATTN_MFPIPE
 #define MI355_ATTN_MFPIPE 1
 #endif
+// S_q <= 128 without bounds: 128-query work-groups (1) or the regular 256-query ones (0)
+#ifndef MI355_ATTN_SHORT
+#define MI355_ATTN_SHORT 1
+#endif
 // Issue priority by progress (1) in the pipelined branch-free sweep: a wave runs the first half of
 // its stages at priority 1 and the rest at 0. Two work-groups share a CU (one wave of each per
 // SIMD), and at equal priority the SIMD issues from the older wave, so of two work-groups that
@@ -309,8 +313,11 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 5, l32 = lane & 31;
   constexpr bool OFFSET = OFFSET_INSTANCE<PIPE, CAUSAL, KMASK> && !REDO;
+  // Bounds need a work-group tile of whole bound chunks (a causal work-group's key range then
+  // ends on a chunk boundary); the 128-query instances of short sequences take none.
+  constexpr bool KB_OK = BM % KB_CHUNK == 0;
   // the key-mask check of the first launch (unmasked instances that take bounds)
-  constexpr bool KCHECK = !KMASK && !REDO && KB_INSTANCE<PIPE, CAUSAL, KMASK>;
+  constexpr bool KCHECK = KB_OK && !KMASK && !REDO && KB_INSTANCE<PIPE, CAUSAL, KMASK>;
   const int64_t wg_id = blockIdx.x + static_cast<int64_t>(gridDim.x) *
                                          (blockIdx.y + static_cast<int64_t>(gridDim.y) * blockIdx.z);
   // the redo launch runs only the work-groups that the sweep launch flagged
@@ -361,11 +368,10 @@ __global__ __launch_bounds__(NW * 64, WPE) void attn_fwd_mfma(AttnArgs p) {
   // in qbound).
   // (not in the causal key-masked instances: at head_dim 64 the bound test takes them past the
   // register budget; the host passes no bounds to them)
-  const bool use_kb = KB_INSTANCE<PIPE, CAUSAL, KMASK> && p.kb != nullptr;
+  const bool use_kb = KB_OK && KB_INSTANCE<PIPE, CAUSAL, KMASK> && p.kb != nullptr;
   float kmax = 0.f;
   const int64_t kend0 = CAUSAL ? ((q_wg + BM) < p.Sk ? (q_wg + BM) : p.Sk) : p.Sk;
   bool kv_skip = false;  // handed to the key-masked redo launch
-  static_assert(BM % KB_CHUNK == 0, "a causal work-group's key range ends on a bound chunk");
   if (use_kb) {
     // causal: only the chunks of the keys this work-group visits, [0, kend) (kend ends on a
     // chunk boundary or at S_k), so that no row's bits depend on a key after its query tile
@@ -1575,6 +1581,33 @@ int launch_mfma(const AttnArgs& a0, bool causal, bool kmask, float* kb_ws, int* 
   return static_cast<int>(hipGetLastError());
 }
 
+// Short query ranges (S_q <= 128, no bounds): work-groups of 128 queries, half the waves of
+// the regular instance. A 256-query work-group there leaves half its waves without queries:
+// official shape 6 (B 10000, S 128, head_dim 32, causal) 591 -> 349 us, the same bits.
+template <typename T, int HD, int NW, int QG>
+int launch_mfma_short(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
+  static_assert(NW * 32 * QG == 128, "128-query work-groups");
+  AttnArgs a = a0;
+  a.n_qtiles = static_cast<int>((a.Sq + 127) / 128);
+  const dim3 block(NW * 64);
+  dim3 grid(a.n_qtiles, static_cast<unsigned>(a.H), static_cast<unsigned>(a.B));
+  const int64_t n = static_cast<int64_t>(a.n_qtiles) * a.H * a.B;
+  const bool flat = n * (NW * 64) <= 0xffffffffLL;  // dispatch size is 32-bit
+  if (causal && !flat) return MI355_E_BAD_SIZE;
+  if (flat) grid = dim3(static_cast<unsigned>(n), 1, 1);
+  if (causal) {
+    if (kmask)
+      launch_one<T, HD, NW, QG, true, true>(a, grid, block, s);
+    else
+      launch_one<T, HD, NW, QG, true, false>(a, grid, block, s);
+  } else if (kmask) {
+    launch_one<T, HD, NW, QG, false, true>(a, grid, block, s);
+  } else {
+    launch_one<T, HD, NW, QG, false, false>(a, grid, block, s);
+  }
+  return static_cast<int>(hipGetLastError());
+}
+
 template <typename T, int HD, int NWK>
 int launch_valu_nwk(const AttnArgs& a0, bool causal, bool kmask, hipStream_t s) {
   constexpr int QT = ValuShape<HD>::QT;
@@ -1739,6 +1772,17 @@ int attn_fwd_impl(int dtype, const void* Q, const void* K, const void* V, void* 
     // room for the redo flags as well: the offset sweep is allowed
     if (workspace_bytes >= redo_offset(B, H, S_k) + redo_flag_bytes(B, H, S_q, head_dim))
       redo = reinterpret_cast<int*>(static_cast<char*>(workspace) + redo_offset(B, H, S_k));
+  }
+  if (MI355_ATTN_SHORT && S_q <= 128 && kb == nullptr) {
+    // (128-query work-groups: half the waves of the regular instances)
+    if (dtype == MI355_F16) {
+      if (head_dim == 32) return launch_mfma_short<_Float16, 32, MI355_ATTN_NW32 / 2, MI355_ATTN_QG32>(a, cz, kmask, s);
+      if (head_dim == 64) return launch_mfma_short<_Float16, 64, MI355_ATTN_NW64 / 2, MI355_ATTN_QG64>(a, cz, kmask, s);
+      return launch_mfma_short<_Float16, 128, MI355_ATTN_NW128 / 2, MI355_ATTN_QG128>(a, cz, kmask, s);
+    }
+    if (head_dim == 32) return launch_mfma_short<__bf16, 32, MI355_ATTN_NW32 / 2, MI355_ATTN_QG32>(a, cz, kmask, s);
+    if (head_dim == 64) return launch_mfma_short<__bf16, 64, MI355_ATTN_NW64 / 2, MI355_ATTN_QG64>(a, cz, kmask, s);
+    return launch_mfma_short<__bf16, 128, MI355_ATTN_NW128 / 2, MI355_ATTN_QG128>(a, cz, kmask, s);
   }
   if (dtype == MI355_F16) {
     if (head_dim == 32)
