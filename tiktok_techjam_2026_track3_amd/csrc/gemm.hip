@@ -653,6 +653,8 @@ __global__ __launch_bounds__(WM* WN * 64, (WM * WN <= 4) ? MI355_GEMM_WPE : 1) v
   }
 #pragma unroll
   for (int b = 0; b < TN; ++b) {
+    // a 32-feature block entirely past N: its staged values are never copied out (wave-uniform)
+    if (n0 + wn * WTN + b * 32 >= p.N) continue;
 #pragma unroll
     for (int i4 = 0; i4 < 4; ++i4) {
       const int n_loc = wn * WTN + b * 32 + 8 * i4 + 4 * g;  // 4 consecutive features
