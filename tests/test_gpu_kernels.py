@@ -207,16 +207,18 @@ def test_attention_key_mask(gpu, dtype, causal):
 @pytest.mark.parametrize("hd", [32, 64, 128])
 @pytest.mark.parametrize("causal", [False, True])
 def test_attention_short_queries_key_mask(gpu, dtype, hd, causal):
-    """S_q <= 128 runs 128-query work-groups (half the waves of the regular instance): key mask
-    with a prefix row, and (non-causal) a key range longer than the query range."""
-    B, S = 3, 128
+    """S_q <= 128 with at least 256 (batch, head) pairs runs 128-query work-groups (half the
+    waves of the regular instance): key mask with a prefix row, and (non-causal) a key range
+    longer than the query range."""
+    B, H, S = 8, 32, 128
     g = torch.Generator().manual_seed(hd + causal)
     mask = torch.rand(B, S, generator=g) > 0.3
     mask[:, 0] = True
     mask[2] = torch.arange(S) < 41
-    _attn_check(gpu, dtype, B, 2, S, S, hd, causal, key_valid=mask, seed=61)
+    _attn_check(gpu, dtype, B, H, S, S, hd, causal, key_valid=mask, seed=61)
+    _attn_check(gpu, dtype, B, H, 77, 77, hd, causal, seed=63)
     if not causal:
-        _attn_check(gpu, dtype, 2, 3, 96, 900, hd, False, seed=62)
+        _attn_check(gpu, dtype, 4, 64, 96, 300, hd, False, seed=62)
 
 
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])

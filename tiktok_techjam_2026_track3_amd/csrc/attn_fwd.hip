@@ -188,7 +188,8 @@ MI355_DEVINL int swz(int r) {
 #ifndef MI355_ATTN_MFPIPE
 #define MI355_ATTN_MFPIPE 1
 #endif
-// S_q <= 128 without bounds: 128-query work-groups (1) or the regular 256-query ones (0)
+// S_q <= 128 without bounds, at least 256 (batch, head) pairs: 128-query work-groups (1) or the
+// regular 256-query ones (0)
 #ifndef MI355_ATTN_SHORT
 #define MI355_ATTN_SHORT 1
 #endif
@@ -1773,8 +1774,10 @@ int attn_fwd_impl(int dtype, const void* Q, const void* K, const void* V, void* 
     if (workspace_bytes >= redo_offset(B, H, S_k) + redo_flag_bytes(B, H, S_q, head_dim))
       redo = reinterpret_cast<int*>(static_cast<char*>(workspace) + redo_offset(B, H, S_k));
   }
-  if (MI355_ATTN_SHORT && S_q <= 128 && kb == nullptr) {
-    // (128-query work-groups: half the waves of the regular instances)
+  if (MI355_ATTN_SHORT && S_q <= 128 && kb == nullptr && B * H >= 256) {
+    // (128-query work-groups: half the waves of the regular instances, each issuing twice the
+    // loads; with fewer (batch, head) pairs than CUs that only lengthens each work-group: C1,
+    // B1 H4, 8.4 -> 9.4 us)
     if (dtype == MI355_F16) {
       if (head_dim == 32) return launch_mfma_short<_Float16, 32, MI355_ATTN_NW32 / 2, MI355_ATTN_QG32>(a, cz, kmask, s);
       if (head_dim == 64) return launch_mfma_short<_Float16, 64, MI355_ATTN_NW64 / 2, MI355_ATTN_QG64>(a, cz, kmask, s);
