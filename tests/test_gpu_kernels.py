@@ -74,6 +74,36 @@ def test_linear_error_bound(gpu, dtype, out_dtype, M, N, K):
     assert _report("linear", err, bound) <= 1.0
 
 
+@pytest.mark.parametrize("out_dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("inplace", [False, True])
+def test_linear_persistent_held_weights_and_residual(gpu, out_dtype, inplace):
+    """The persistent kernel on a one-column problem whose K is one ring turn (300000 x 128 x
+    128: 1172 tiles, W's stages held in the ring after the first tile) with the residual in its
+    epilogue (requested two chunks at a time; in place: R is C), against fp64, and the row mask
+    with zeroed rows."""
+    ops = _ops()
+    M, N, K = 300000, 128, 128
+    a = _rand((M, K), torch.float16, 11)
+    w = _rand((N, K), torch.float16, 12, scale=K ** -0.5)
+    b = _rand((N,), torch.float32, 13, scale=0.1)
+    r = _rand((M, N), out_dtype, 14)
+    rows = torch.rand(M, generator=torch.Generator().manual_seed(15)) > 0.2
+    print(f"persistent held-W linear out={out_dtype} inplace={inplace}", flush=True)
+    gr = r.to(gpu)
+    out = ops.linear(a.to(gpu), w.to(gpu), b.to(gpu), out_dtype=out_dtype, residual=gr,
+                     out=gr if inplace else None, row_valid=rows.to(gpu), zero_masked_rows=True)
+    out = out.cpu().double()
+    a64, w64 = a.double(), w.double()
+    proj = a64 @ w64.T + b.double()
+    # the projection rounded to the output type, then the residual added and rounded again
+    ref = proj + r.double()
+    bound = (UNIT[out_dtype] * (proj.abs() + ref.abs()) + 4 * K * 2.0 ** -24 * (a64.abs() @ w64.abs().T)
+             + 1e-7)
+    err = (out - ref).abs()
+    assert torch.all(out[~rows] == 0)
+    assert _report("linear+residual", err[rows], bound[rows]) <= 1.0
+
+
 @pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
 def test_linear_strided_input_and_row_mask(gpu, dtype):
     ops = _ops()
