@@ -328,10 +328,11 @@ def test_attention_other_head_dims_masked_packed(gpu, dtype, hd, causal):
 # --------------------------------------------------------------------------------- int8
 @pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32])
 @pytest.mark.parametrize("mode", [0, 1])
-@pytest.mark.parametrize("K", [512, 4096, 4000, 16384])
+@pytest.mark.parametrize("K", [512, 4096, 4000, 8192, 16384, 32768])
 def test_quant_rows_bit_exact(gpu, dtype, mode, K):
     """Row lengths that keep the row in registers (64 * 2^i 16-byte chunks up to 16 per lane:
-    512 and 4096, and 16384 for fp32) and that take the two-pass kernel (4000; 16384 16-bit)."""
+    512 and 4096, 8192 16-bit) and that take the two-pass kernel (4000; 16384 and 32768 16-bit,
+    8192 and more fp32)."""
     ops = _ops()
     x = _rand((300, K), dtype, 41, scale=0.7)
     x[3] = 0                                   # zero row exercises the clamp
