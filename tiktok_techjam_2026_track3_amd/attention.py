@@ -319,14 +319,15 @@ class SelfAttention(nn.Module):
         """``x + self(norm(x), valid_token_mask, causal)``: the attention half of
         BaselineTransformerBlock.forward (torch_transformer_benchmark.py:139).
 
-        For fp32 / fp16 inputs the LayerNorm is folded into the QKV projection (``fold_norm``,
-        ``folds_norm``; the reference's fused
+        For fp16 inputs (and fp32 inputs on fp32 projection operands) the LayerNorm is folded
+        into the QKV projection (``fold_norm``, ``folds_norm``; the reference's fused
         LN-prologue QKV kernels Project/kernels/k024_cuda_tuned.py:94-197 and
         Project/submission/dispatcher_region.py:343-399): a row-statistics pass, then the
         projection of the raw x with gamma folded into the weights and the mean / rstd / beta
         applied in its epilogue, so the normalised rows are never written. With
-        ``fold_norm = False`` it runs as its own row kernel (fp32 statistics, rounded to x's
-        dtype as nn.LayerNorm's output is). The residual add is fused into the out projection's
+        ``fold_norm = False``, for bf16 and for fp32 inputs on fp16 operands it runs as its own
+        row kernel (fp32 statistics, rounded to x's dtype as nn.LayerNorm's output is, or to the
+        fp16 operand type). The residual add is fused into the out projection's
         epilogue, where the projection is rounded to x's dtype before the add, as in the
         reference; rows masked out keep x. ``marks`` as for ``run``; the unfolded form has an
         extra "norm" stage before "qkv".

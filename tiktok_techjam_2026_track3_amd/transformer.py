@@ -123,7 +123,7 @@ def block_forward(block: nn.Module, x: torch.Tensor, valid_token_mask: Optional[
     kernels, for any module with the block's attributes whose ``attention`` is a SelfAttention
     (or an Int8SelfAttention: the W8A8 block).
 
-    With ``attention.folds_norm(dtype)`` (fp32 / fp16 by default) norm1 is folded into the QKV projection and norm2
+    With ``attention.folds_norm(dtype)`` (fp16 models by default) norm1 is folded into the QKV projection and norm2
     into ffn_in (row-statistics pass + projection epilogue, ``ops.layernorm_linear``), so neither
     normalised activation is written. ``marks(stage)`` is called before each launch ("qkv",
     "attn", "out", "ffn_in", "ffn_out"; unfolded, "norm" and "norm2" before the LayerNorm
