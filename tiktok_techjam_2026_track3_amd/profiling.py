@@ -14,6 +14,10 @@ reports with the commands that produced them):
 * ``util DIR...`` -- per-kernel compute utilisation from one or more ``--pmc`` runs of the same
   command (counters merged by kernel): MFMA busy, MFMA/VALU co-execution, VALU activity, the
   shader clock, and the MFMA operation count, each with the formula it is computed by.
+* ``gemm-loop``    -- runs one projection shape back to back for a fixed time, first on this
+  build's GEMM (``ops.linear``), then, after an idle gap, on torch's ``F.linear`` (hipBLASLt),
+  and prints each one's rate and end time: a steady load for reading the package power and
+  clock with ``amd-smi`` / ``rocm-smi`` beside it (GPU box only).
 
 Usage::
 
@@ -260,6 +264,41 @@ def traffic(config: str, kernel: str, fetch: str, write: str, copy_fetch: str, c
             "copy_bytes": copy_bytes, "copy_fetch_factor": f_fetch, "copy_write_factor": f_write}
 
 
+def gemm_loop(shape: str, dtype: str, out_dtype: str, seconds: float, gap: float) -> None:
+    """The ``gemm-loop`` report (see the module docstring)."""
+    import time
+    import torch
+    from . import ops
+    M, N, K = (int(v) for v in shape.split(","))
+    dt, odt = getattr(torch, dtype), getattr(torch, out_dtype)
+    dev = torch.device("cuda:0")
+    g = torch.Generator(device=dev).manual_seed(0)
+    a = torch.randn(M, K, device=dev, generator=g).to(dt)
+    w = (torch.randn(N, K, device=dev, generator=g) * 0.02).to(dt)
+    b = torch.randn(N, device=dev, generator=g) * 0.02
+    out = torch.empty(M, N, device=dev, dtype=odt)
+    runs = (("this build", lambda: ops.linear(a, w, b, out=out, out_dtype=odt)),
+            ("hipBLASLt", lambda: torch.nn.functional.linear(a, w, b.to(dt))))
+    for i, (name, f) in enumerate(runs):
+        f()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        t0, n = time.time(), 0
+        e0.record()
+        while time.time() - t0 < seconds:
+            for _ in range(50):
+                f()
+            n += 50
+            torch.cuda.synchronize()
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / n
+        print(f"{name}: {ms:.4f} ms per GEMM, {2.0 * M * N * K / ms / 1e9:.1f} TFLOP/s over {n} calls; "
+              f"ended at {time.time():.1f}", flush=True)
+        if i == 0:
+            time.sleep(gap)
+
+
 def main(argv=None) -> int:
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     sub = ap.add_subparsers(dest="cmd", required=True)
@@ -277,8 +316,16 @@ def main(argv=None) -> int:
     t.add_argument("--json-out", help="merge the record into this JSON file (keyed by config)")
     u = sub.add_parser("util")
     u.add_argument("dirs", nargs="+")
+    gl = sub.add_parser("gemm-loop")
+    gl.add_argument("--shape", default="32768,6144,2048", help="M,N,K")
+    gl.add_argument("--dtype", default="bfloat16")
+    gl.add_argument("--out-dtype", default="float16")
+    gl.add_argument("--seconds", type=float, default=12.0)
+    gl.add_argument("--gap", type=float, default=3.0)
     a = ap.parse_args(argv)
-    if a.cmd == "stats":
+    if a.cmd == "gemm-loop":
+        gemm_loop(a.shape, a.dtype, a.out_dtype, a.seconds, a.gap)
+    elif a.cmd == "stats":
         print_stats(a.dir, a.stage)
     elif a.cmd == "pmc":
         print_pmc(a.dir)
